@@ -1,0 +1,230 @@
+"""Benchmark: 64-request ragged talker decode step on one MI355X.
+
+Workload (the talker decode-attention step): 64 concurrent requests with context lengths
+c_b = torch.randint(64, 1025, (64,)) under seed 0 (sum 32,718), a packed bf16 KV arena
+(2*28 planes, 64 slots, 8 KV heads, capacity 1024, head_dim 128), 16 query heads, RoPE
+theta 1e6.  One step = 28 layers; each layer is one fused HIP launch doing RoPE of q and of
+the new key, the paired K/V write at position c_b and ragged GQA decode attention over
+c_b + 1 keys.  The 28 launches of a step are captured once into a HIP graph and replayed.
+Inputs are synthetic (seeded random, resident in HBM before timing).
+
+Prints one JSON line: tokens/s (64 tokens per step), the dominant kernel's roofline
+(algorithmic bytes per launch / average launch time against 8 TB/s) and the CPU baseline
+(the reference's torch decode layer on this host's cores, bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import __graft_entry__  # noqa: E402
+
+LAYERS, BATCH, HQ, HKV, D, CAPACITY = 28, 64, 16, 8, 128, 1024
+PEAK_HBM_GBS = 8000.0
+TRAFFIC_SUMMARY = ROOT / "profiles" / "decode_step_talker64_hbm_traffic.md"
+
+
+def algorithmic_bytes(contexts: torch.Tensor) -> int:
+    """Bytes one fused layer launch must move: arena K/V rows 0..c_b-1 read, the new K/V rows
+    read from the QKV projection and written to the arena, Q read, O written, cos/sin rows
+    read, positions read."""
+    row = HKV * D * 2                       # one token of one plane, bf16
+    arena_read = int(contexts.sum()) * row * 2
+    new_kv = BATCH * row * 2 * 2            # read + write, K and V
+    q_o = BATCH * HQ * D * 2 * 2
+    cos_sin = BATCH * D * 2 * 2
+    return arena_read + new_kv + q_o + cos_sin + BATCH * 8
+
+
+def attention_bytes(contexts: torch.Tensor) -> int:
+    """Bytes of the non-fused attention launch: arena K/V rows 0..c_b read, Q read, O written."""
+    return (int(contexts.sum()) + BATCH) * HKV * D * 2 * 2 + BATCH * HQ * D * 2 * 2 + BATCH * 8
+
+
+def read_traffic():
+    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (committed summary)."""
+    if not TRAFFIC_SUMMARY.exists():
+        return None
+    text = TRAFFIC_SUMMARY.read_text()
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", text)
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(seconds: float):
+    """The reference's torch decode layer (scatter_ write, eager bf16 RoPE, SDPA under the
+    0/finfo.min context mask) on this host, one layer of the same 64-request workload."""
+    from oracle import torch_path
+
+    threads = torch.get_num_threads()
+    gen = torch.Generator().manual_seed(0)
+    contexts = torch.randint(64, 1025, (BATCH,), generator=gen)
+    arena_k = torch.randn(BATCH, HKV, CAPACITY, D, generator=gen).bfloat16()
+    arena_v = torch.randn(BATCH, HKV, CAPACITY, D, generator=gen).bfloat16()
+    qkv = torch.randn(BATCH, 1, (HQ + 2 * HKV) * D, generator=gen).bfloat16()
+    q = qkv[..., :HQ * D].view(BATCH, 1, HQ, D)
+    k = qkv[..., HQ * D:(HQ + HKV) * D].view(BATCH, 1, HKV, D)
+    v = qkv[..., (HQ + HKV) * D:].view(BATCH, 1, HKV, D)
+    angle = (contexts.float()[:, None] * (1.0 / (1e6 ** (torch.arange(0, D, 2).float() / D)))[None])
+    emb = torch.cat([angle, angle], -1)
+    cos, sin = emb.cos().bfloat16()[:, None], emb.sin().bfloat16()[:, None]
+    times = []
+    deadline = time.perf_counter() + seconds
+    with torch.inference_mode():
+        torch_path.decode_layer(q, k, v, cos, sin, arena_k, arena_v, contexts)  # warm-up
+        while time.perf_counter() < deadline or len(times) < 3:
+            t0 = time.perf_counter()
+            torch_path.decode_layer(q, k, v, cos, sin, arena_k, arena_v, contexts)
+            times.append(time.perf_counter() - t0)
+            if len(times) >= 200:
+                break
+    times.sort()
+    layer_s = times[len(times) // 2]
+    return {"value": BATCH / (LAYERS * layer_s), "unit": "tokens/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"median of {len(times)} runs of one talker layer (64 requests, capacity "
+                       f"{CAPACITY}, bf16, torch {threads} threads) = {layer_s * 1e3:.2f} ms, "
+                       f"scaled to a 28-layer step")}
+
+
+def main():
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--splits", type=int, default=0, help="workgroups per KV head (0 = default)")
+    parser.add_argument("--cpu-seconds", type=float, default=10.0)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--calibrate-bytes", type=int, default=0,
+                        help="after timing, launch the plain copy kernel on this many bytes "
+                             "(HBM counter calibration under rocprofv3)")
+    args = parser.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(decode would shard by request slot, one arena per GPU)", file=sys.stderr)
+        sys.exit(2)
+
+    pkg = __graft_entry__.import_package()
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    gen = torch.Generator().manual_seed(0)
+    contexts = torch.randint(64, 1025, (BATCH,), generator=gen)
+    positions = contexts.to(device)
+    dgen = torch.Generator(device=device).manual_seed(1)
+    arena = torch.randn(2 * LAYERS, BATCH, HKV, CAPACITY, D, generator=dgen, device=device,
+                        dtype=torch.bfloat16)
+    qkv = torch.randn(LAYERS, BATCH, 1, (HQ + 2 * HKV) * D, generator=dgen, device=device,
+                      dtype=torch.bfloat16)
+    cos, sin = pkg.rope_tables(positions, D)
+    out = torch.empty(LAYERS, BATCH, 1, HQ, D, device=device, dtype=torch.bfloat16)
+    views = []
+    for layer in range(LAYERS):
+        row = qkv[layer]
+        views.append((row[..., :HQ * D].view(BATCH, 1, HQ, D),
+                      row[..., HQ * D:(HQ + HKV) * D].view(BATCH, 1, HKV, D),
+                      row[..., (HQ + HKV) * D:].view(BATCH, 1, HKV, D),
+                      arena[layer], arena[LAYERS + layer], out[layer]))
+
+    def step():
+        for q, k, v, ak, av, o in views:
+            pkg.decode_step(q, k, v, ak, av, positions, cos, sin, out=o, splits_per_head=args.splits)
+
+    step()  # eager: sizes the workspace before capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    stream = torch.cuda.current_stream()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(args.steps):
+        graph.replay()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = start.elapsed_time(stop)
+    ms_per_step = gpu_ms / args.steps
+    launch_us = ms_per_step * 1e3 / LAYERS
+    bytes_per_launch = algorithmic_bytes(contexts)
+    achieved = bytes_per_launch / (launch_us * 1e-6) / 1e9
+
+    # attention alone: the non-fused kernel over the already-written arena, same graph method
+    q0 = views[0][0].contiguous()
+    attn_graph = torch.cuda.CUDAGraph()
+    pkg.decode_attention(q0, arena[0], arena[LAYERS], positions, splits_per_head=args.splits)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(attn_graph):
+        for layer in range(LAYERS):
+            pkg.decode_attention(q0, arena[layer], arena[LAYERS + layer], positions,
+                                 out=out[layer], splits_per_head=args.splits)
+    attn_graph.replay()
+    torch.cuda.synchronize()
+    reps = max(1, args.steps // 4)
+    start.record(stream)
+    for _ in range(reps):
+        attn_graph.replay()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    attn_us = start.elapsed_time(stop) * 1e3 / (reps * LAYERS)
+
+    if args.calibrate_bytes > 0:
+        n = args.calibrate_bytes // 16 * 16
+        src = torch.empty(n, dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            status = pkg.library().q3t_copy_bytes(dst.data_ptr(), src.data_ptr(), n, stream.cuda_stream)
+            if status != 0:
+                raise RuntimeError("calibration copy failed")
+        torch.cuda.synchronize()
+
+    traffic = read_traffic()
+    result = {
+        "metric": "decode-attn tokens/s + achieved HBM GB/s, 64-req ragged talker step, 1 GPU",
+        "value": BATCH * args.steps / (gpu_ms / 1e3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) K/V arena, QKV rows; seed-0 context lengths)",
+        "config": {"workload": "talker ragged decode step: 64 requests, contexts U[64,1024] "
+                               "(seed 0, sum 32718), 28 layers, 16q/8kv heads, head_dim 128, "
+                               "arena capacity 1024, fused RoPE + KV write + GQA decode",
+                   "global_batch": BATCH, "layers": LAYERS, "context_sum": int(contexts.sum()),
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBS,
+                     "traffic": traffic},
+        "detail": {"kernel": "decode_attention_kernel<bf16,128,G2,SQ1,fused>",
+                   "algorithmic_bytes_per_launch": bytes_per_launch,
+                   "us_per_layer_launch": launch_us,
+                   "us_per_layer_attention_only": attn_us,
+                   "attention_only_GBs": attention_bytes(contexts) / (attn_us * 1e-6) / 1e9,
+                   "splits_per_head": args.splits or "default",
+                   "wall_s_timed_region": wall},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,222 @@
+/*
+ * qwen3tts_amd.h - C ABI of the MI355X (gfx950) continuous-batching attention path.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes, and an
+ * optional HIP stream (`void *stream`, a hipStream_t; NULL = the legacy default stream).
+ * Nothing here allocates device memory, synchronises the host or touches PyTorch, so
+ * every call may be captured into a HIP graph.  Arguments are validated on the host
+ * before anything is launched: a rejected call returns a negative status and writes
+ * nothing.  A positive status is the hipError_t reported by the launch.
+ *
+ * Layouts follow the reference engine (InferMatrixLab/qwen3-tts-rsi-engine):
+ *   - KV arena per layer: (slots, kv_heads, capacity, head_dim), contiguous rows;
+ *     the packed arena stacks 2*layers of them, keys first
+ *     (qwen3_tts_engine/continuous.py:107-113).
+ *   - Queries and new keys/values are BSND rows of the fused QKV projection
+ *     (qwen3_tts_engine/packed_attention.py:42-45), passed with explicit strides.
+ *
+ * Strides are in ELEMENTS, never bytes.
+ */
+#ifndef QWEN3TTS_AMD_H
+#define QWEN3TTS_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------------------ */
+#define Q3T_OK 0
+#define Q3T_EINVAL (-1)        /* malformed argument (null pointer, bad size or stride)    */
+#define Q3T_EUNSUPPORTED (-2)  /* well-formed but outside the compiled kernel variants      */
+#define Q3T_EWORKSPACE (-3)    /* workspace pointer missing or too small                     */
+
+/* ---- element types ----------------------------------------------------------------- */
+#define Q3T_BF16 0
+#define Q3T_F16 1
+#define Q3T_F32 2
+#define Q3T_BOOL 3  /* masks only: nonzero = attend, as a torch bool SDPA mask */
+
+/* Human-readable text for a status returned by any entry point. */
+const char *q3t_status_string(int status);
+
+/* ABI revision of this header; bumps on any incompatible change. */
+int q3t_abi_version(void);
+
+/* ---- KV arena writes and copies ------------------------------------------------------ */
+
+/*
+ * Paired K/V write of `tokens` new rows per request into a slot arena:
+ *   target_keys  [b, h, positions[b] + t, :] = keys  [b, h, t, :]
+ *   target_values[b, h, positions[b] + t, :] = values[b, h, t, :]
+ * for b < batch, h < heads, t < tokens.  Bit-exact copy of `elem_size`-byte elements.
+ * Source strides (b, h, t) are free (the fused QKV row stride is (Hq+2*Hkv)*D);
+ * the last dimension must be unit-stride.  Targets are (batch, heads, capacity, width)
+ * with strides (b, h, s) given in target_strides.  Rows whose position falls outside
+ * [0, capacity) are skipped on the device (the reference leaves them undefined).
+ *
+ * Replaces: SlotCache.update's scatter_ / npu_scatter_nd_update_ (continuous.py:152-166),
+ * kv_triton_ascend.write (kv_triton_ascend.py:39-64), PredictorCache.update
+ * (predictor.py:19-24) with tokens = 2 at step 0.
+ */
+int q3t_kv_write(const void *keys, const void *values, void *target_keys, void *target_values,
+                 const int64_t *positions, int64_t batch, int64_t heads, int64_t tokens,
+                 int64_t width, int64_t elem_size, const int64_t key_strides[3],
+                 const int64_t value_strides[3], const int64_t target_strides[3],
+                 int64_t capacity, void *stream);
+
+/*
+ * Strided element copy over up to 5 dimensions: dst[i...] = src[i...].
+ * Used for the packed prefix copy, slot compaction and arena regrowth.
+ * Replaces: copy_packed_prefix (packed_kv.py:6-31), SlotArena.load / move
+ * (continuous.py:118-128), ensure_capacity's copy (continuous.py:362-363).
+ */
+int q3t_copy_strided(void *dst, const void *src, int64_t elem_size, int ndim,
+                     const int64_t *sizes, const int64_t *dst_strides,
+                     const int64_t *src_strides, void *stream);
+
+/* Plain contiguous byte copy (also the calibration kernel for HBM counters). */
+int q3t_copy_bytes(void *dst, const void *src, int64_t nbytes, void *stream);
+
+/* ---- rotary position embedding ------------------------------------------------------ */
+
+/*
+ * Rotate-half RoPE on BSND rows with torch-eager rounding (Q3T_BF16 or Q3T_F32):
+ *   bf16: y1 = bf16(bf16(x1*c1) + bf16(-x2*s1)),  y2 = bf16(bf16(x2*c2) + bf16(x1*s2))
+ *   fp32: the same with every product and sum rounded to fp32 separately (no FMA)
+ * x, y: (rows, heads, width) contiguous; cos, sin: (rows, width) contiguous, same dtype.
+ * width in {64, 128}.  Replaces: rotary_triton_ascend.rotary (rotary_triton_ascend.py:29-44)
+ * and apply_rotary_pos_emb on the talker's equal-axis positions (packed_attention.py:62-65).
+ */
+int q3t_rotary(const void *x, const void *cos, const void *sin, void *y, int64_t rows,
+               int64_t heads, int64_t width, int64_t dtype, void *stream);
+
+/*
+ * Default-RoPE cos/sin tables: for n positions and width = 2*half,
+ *   f = inv_freq[i] * (float)positions[r];  cos[r, i] = cos[r, i + half] = cos(f)*scaling
+ * (same for sin), stored as dtype (Q3T_BF16, rounded to nearest even, or Q3T_F32).
+ * inv_freq is a device fp32 array of `half` entries computed by the caller.
+ * Replaces: the talker rotary_emb cos/sin (continuous.py:193, prefill_graph.py:38).
+ */
+int q3t_rope_tables(const int64_t *positions, int64_t n, const float *inv_freq, int64_t half,
+                    float scaling, int64_t dtype, void *cos, void *sin, void *stream);
+
+/* ---- attention ----------------------------------------------------------------------- */
+
+/*
+ * Ragged grouped-query decode attention over a slot arena.
+ * Request b has query_len queries at positions p_b - query_len + 1 ... p_b, where
+ * p_b = positions[b]; keys 0 ... p_b of its slot are read (the reference's additive mask
+ * `j <= pos[b]`, continuous.py:191-192).  Without a mask, query i attends keys
+ * 0 ... p_b - query_len + 1 + i (the predictor's 2x2 causal step, continuous.py:39-40);
+ * with a mask (batch, query_len, ctx) the mask alone decides, added to the scaled scores
+ * as SDPA does (bool masks: nonzero attends).
+ * Query head hq reads KV head hq / (q_heads / kv_heads).
+ * Work is split over the keys of every (request, kv head) ("split-K"); partial softmax
+ * states are merged in LDS within a workgroup and across workgroups through `workspace`.
+ *
+ * fused != 0 additionally performs, for query_len == 1:
+ *   - RoPE of the query rows and of the new key with cos/sin rows (bf16-exact, as q3t_rotary),
+ *   - the paired K/V write of the new (rotated) key and value at positions[b],
+ * and uses the new key/value for key p_b without re-reading the arena.  Then `query`,
+ * `new_key`, `new_value` are the un-rotated BSND rows of the QKV projection.
+ * Replaces: PackedAttention.forward's RoPE + cache update + attention dispatch
+ * (packed_attention.py:46-84), npu_attention.attention (npu_attention.py:11-26).
+ */
+typedef struct q3t_decode_args {
+    /* sizes */
+    int64_t batch, query_len, q_heads, kv_heads, head_dim;
+    int64_t ctx;        /* keys addressable per slot (arena capacity or context view) */
+    int64_t dtype;      /* Q3T_BF16 or Q3T_F32 (fused requires Q3T_BF16) */
+    float scale;        /* softmax scale, normally head_dim ** -0.5 */
+    int32_t fused;
+    /* query (batch, query_len, q_heads, head_dim) */
+    const void *query;
+    int64_t q_stride_b, q_stride_s, q_stride_h;
+    /* arena views for this layer: key (b, h, j) at base + off_b + h*stride_h + j*stride_t,
+       off_b = kv_offsets ? kv_offsets[b] : b*stride_b (elements) */
+    void *keys, *values;
+    int64_t k_stride_b, k_stride_h, k_stride_t;
+    int64_t v_stride_b, v_stride_h, v_stride_t;
+    const int64_t *kv_offsets; /* optional, device, (batch,) */
+    const int64_t *positions;  /* device, (batch,): last query position p_b */
+    /* optional additive mask (batch, query_len, ctx); dtype = mask_dtype; NULL = none */
+    const void *mask;
+    int64_t mask_dtype, mask_stride_b, mask_stride_s, mask_stride_t;
+    /* output (batch, query_len, q_heads, head_dim), same dtype as query */
+    void *out;
+    int64_t o_stride_b, o_stride_s, o_stride_h;
+    /* fused only: new key/value rows (batch, kv_heads, head_dim) and cos/sin (batch, head_dim) */
+    const void *new_key, *new_value;
+    int64_t nk_stride_b, nk_stride_h, nv_stride_b, nv_stride_h;
+    const void *cos, *sin;
+    int64_t cs_stride_b;
+    /* split-K workspace: a fixed 256 KiB counter region (kv_heads * batch <= 65536) then the
+       partial states; zero-filled before first use, its counters left zeroed by every launch */
+    void *workspace;
+    int64_t workspace_bytes;
+    int64_t splits_per_head; /* workgroups per kv head; <= 0 selects the default */
+} q3t_decode_args;
+
+/* Bytes of workspace needed by q3t_decode_attention for these sizes. */
+int64_t q3t_decode_workspace_bytes(int64_t batch, int64_t query_len, int64_t q_heads,
+                                   int64_t kv_heads, int64_t head_dim,
+                                   int64_t splits_per_head);
+
+int q3t_decode_attention(const q3t_decode_args *args, void *stream);
+
+/*
+ * Varlen causal prefill attention with GQA on bf16 MFMA tiles.
+ * Requests are packed along the token axis by cu_seqlens (batch + 1, int32, device):
+ * query rows (tokens, q_heads, head_dim); key/value rows are read from the slot arena
+ * (slot = kv_slots ? kv_slots[b] : b) at positions 0 ... len_b - 1, with strides as in
+ * q3t_decode_args.  Query token i of request b attends keys 0 ... i.
+ * Replaces: PrefillGraph.compute's padded causal attention (prefill_graph.py:31-50) for
+ * the valid rows of each request.
+ */
+typedef struct q3t_prefill_args {
+    int64_t batch, total_tokens, max_seqlen, q_heads, kv_heads, head_dim;
+    float scale;
+    const int32_t *cu_seqlens;     /* device (batch + 1) */
+    const void *query;             /* (tokens, q_heads, head_dim) bf16 */
+    int64_t q_stride_t, q_stride_h;
+    const void *keys, *values;     /* arena views */
+    int64_t k_stride_b, k_stride_h, k_stride_t;
+    int64_t v_stride_b, v_stride_h, v_stride_t;
+    const int64_t *kv_slots;       /* optional device (batch,) */
+    void *out;                     /* (tokens, q_heads, head_dim) bf16 */
+    int64_t o_stride_t, o_stride_h;
+} q3t_prefill_args;
+
+int q3t_prefill_attention(const q3t_prefill_args *args, void *stream);
+
+/*
+ * Prefill prologue: RoPE of packed query/key rows at positions 0 ... len_b - 1 (cos/sin
+ * rows indexed by token) and the paired write of rotated keys and raw values into the
+ * arena slot of each request.  q_out receives the rotated queries.
+ * Replaces: the per-layer RoPE + DynamicCache fill of PrefillGraph.compute
+ * (prefill_graph.py:38-43) and the later copy_packed_prefix into the arena
+ * (continuous.py:468-469).
+ */
+typedef struct q3t_prefill_rope_write_args {
+    int64_t batch, total_tokens, q_heads, kv_heads, head_dim, capacity;
+    const int32_t *cu_seqlens;
+    const void *query; int64_t q_stride_t, q_stride_h;
+    const void *key;   int64_t k_stride_t, k_stride_h;
+    const void *value; int64_t v_stride_t, v_stride_h;
+    const void *cos, *sin; int64_t cs_stride_t;
+    void *q_out; int64_t qo_stride_t, qo_stride_h;
+    void *arena_keys, *arena_values;
+    int64_t a_stride_b, a_stride_h, a_stride_t;
+    const int64_t *kv_slots;
+} q3t_prefill_rope_write_args;
+
+int q3t_prefill_rope_write(const q3t_prefill_rope_write_args *args, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWEN3TTS_AMD_H */

@@ -1,0 +1,258 @@
+"""Grouped-query attention on the GPU: decode (split-K), fused decode step, drop-in dispatch.
+
+* ``decode_attention`` - ragged GQA over a slot arena: request b attends keys
+  0 ... positions[b] of its slot (the mask ``j <= pos[b]`` of SlotGraph.compute,
+  qwen3_tts_engine/continuous.py:191-192), optionally under an SDPA-style mask.
+* ``decode_step`` - one launch doing RoPE of q and the new key, the paired K/V write at
+  positions[b] and the attention (PackedAttention.forward's decode path,
+  qwen3_tts_engine/packed_attention.py:46-84).
+* ``attention`` - drop-in for ``npu_attention.attention``
+  (qwen3_tts_engine/npu_attention.py:11-26): same signature, errors and output layout.
+* ``prefill_attention`` - varlen causal attention over cu_seqlens on bf16 MFMA tiles.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_WORKSPACES: dict = {}
+_RETIRED: list = []
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Zero-filled split-K workspace shared by every launch on ``device``.
+
+    Kernels leave its counters zeroed, so one buffer serves all sequential launches on a
+    stream.  Launches that overlap on two streams of one device must not share it.
+    It grows only outside graph capture; earlier buffers stay alive for captured graphs."""
+    current = _WORKSPACES.get(device)
+    if current is not None and current.numel() >= nbytes:
+        return current
+    if torch.cuda.is_current_stream_capturing():
+        raise ValueError('decode workspace must be sized by an eager call before graph capture')
+    grown = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+    if current is not None:
+        _RETIRED.append(current)
+    _WORKSPACES[device] = grown
+    return grown
+
+
+def _mask_view(mask, batch, query_len, ctx):
+    """SDPA-style mask broadcastable to (batch, 1, query_len, ctx) -> (batch, query_len, ctx)."""
+    if mask.ndim == 4:
+        if mask.shape[1] != 1:
+            raise ValueError('per-head attention masks are not supported')
+        mask = mask[:, 0]
+    elif mask.ndim == 2:
+        mask = mask[None]
+    if mask.ndim != 3 or mask.shape[-1] != ctx:
+        raise ValueError('attention mask must end in the key dimension')
+    if mask.dtype not in _lib.DTYPE_CODES:
+        raise ValueError('attention mask must be bool, bf16, fp16 or fp32')
+    return mask.expand(batch, query_len, ctx)
+
+
+def _run_decode(args: _lib.DecodeArgs, device: torch.device, what: str) -> None:
+    lib = _lib.library()
+    with torch.cuda.device(device):
+        need = lib.q3t_decode_workspace_bytes(args.batch, args.query_len, args.q_heads,
+                                              args.kv_heads, args.head_dim, args.splits_per_head)
+        if need < 0:
+            raise ValueError(f'{what}: invalid sizes')
+        ws = workspace(device, need)
+        args.workspace = ws.data_ptr()
+        args.workspace_bytes = ws.numel()
+        status = lib.q3t_decode_attention(args, _lib.stream_handle(device))
+    _lib.check(status, what)
+
+
+def decode_attention(query, keys, values, positions, *, scale=None, mask=None, kv_offsets=None,
+                     out=None, splits_per_head=0):
+    """query (B, S, Hq, D) BSND; keys/values (B, Hkv, ctx, D) views of the arena (or, with
+    ``kv_offsets``, any base tensor whose request rows start at those element offsets);
+    positions (B,) int64: the last query position of each request.  Returns (B, S, Hq, D)."""
+    if query.ndim != 4 or keys.ndim != 4 or values.shape != keys.shape:
+        raise ValueError('expected BSND query and BNSD key/value views')
+    batch, qlen, q_heads, head_dim = query.shape
+    kv_heads, ctx = keys.shape[1], keys.shape[2]
+    if kv_offsets is None and keys.shape[0] < batch:
+        raise ValueError('key/value views must cover every request')
+    if keys.shape[3] != head_dim or q_heads % kv_heads:
+        raise ValueError('head_dim mismatch or q_heads not a multiple of kv_heads')
+    if query.dtype not in (torch.bfloat16, torch.float32) or keys.dtype != query.dtype or values.dtype != query.dtype:
+        raise ValueError('decode attention supports bf16 or fp32 tensors of one dtype')
+    if positions.shape != (batch,) or positions.dtype != torch.int64:
+        raise ValueError('positions must be an int64 (batch,) tensor')
+    if query.stride(3) != 1 or keys.stride(3) != 1 or values.stride(3) != 1:
+        raise ValueError('rows must be unit-stride along head_dim')
+    tensors = [query, keys, values, positions] + ([kv_offsets] if kv_offsets is not None else [])
+    device = _lib.require_gpu(*tensors)
+    if out is None:
+        out = torch.empty(batch, qlen, q_heads, head_dim, device=device, dtype=query.dtype)
+    elif out.shape != (batch, qlen, q_heads, head_dim) or out.dtype != query.dtype or out.stride(3) != 1:
+        raise ValueError('out must be (B, S, Hq, D) of the query dtype')
+    a = _lib.DecodeArgs()
+    a.batch, a.query_len, a.q_heads, a.kv_heads, a.head_dim = batch, qlen, q_heads, kv_heads, head_dim
+    a.ctx = ctx
+    a.dtype = _lib.DTYPE_CODES[query.dtype]
+    a.scale = head_dim ** -0.5 if scale is None else float(scale)
+    a.fused = 0
+    a.query = query.data_ptr()
+    a.q_stride_b, a.q_stride_s, a.q_stride_h = query.stride()[:3]
+    a.keys, a.values = keys.data_ptr(), values.data_ptr()
+    a.k_stride_b, a.k_stride_h, a.k_stride_t = keys.stride()[:3]
+    a.v_stride_b, a.v_stride_h, a.v_stride_t = values.stride()[:3]
+    if kv_offsets is not None:
+        if kv_offsets.shape != (batch,) or kv_offsets.dtype != torch.int64:
+            raise ValueError('kv_offsets must be an int64 (batch,) tensor')
+        a.kv_offsets = kv_offsets.data_ptr()
+    a.positions = positions.data_ptr()
+    if mask is not None:
+        m = _mask_view(mask.to(device), batch, qlen, ctx)
+        a.mask = m.data_ptr()
+        a.mask_dtype = _lib.DTYPE_CODES[m.dtype]
+        a.mask_stride_b, a.mask_stride_s, a.mask_stride_t = m.stride()
+    a.out = out.data_ptr()
+    a.o_stride_b, a.o_stride_s, a.o_stride_h = out.stride()[:3]
+    a.splits_per_head = int(splits_per_head or 0)
+    _run_decode(a, device, 'decode attention')
+    return out
+
+
+def decode_step(query, new_key, new_value, key_arena, value_arena, positions, cos, sin, *,
+                scale=None, out=None, splits_per_head=0):
+    """Fused one-token decode for a layer.
+
+    query (B, 1, Hq, D), new_key/new_value (B, 1, Hkv, D): un-rotated bf16 rows (views of the
+    fused QKV projection are fine); key_arena/value_arena (slots >= B, Hkv, C, D) contiguous;
+    positions (B,) int64; cos/sin (B, D) or (B, 1, D) bf16.  Writes the rotated key and the
+    value at positions[b] and returns the attention output (B, 1, Hq, D)."""
+    if query.ndim != 4 or query.shape[1] != 1 or new_key.ndim != 4 or new_key.shape[1] != 1:
+        raise ValueError('fused decode expects one-token BSND rows')
+    batch, _, q_heads, head_dim = query.shape
+    if new_value.shape != new_key.shape or new_key.shape[0] != batch or new_key.shape[3] != head_dim:
+        raise ValueError('new key/value rows must match the query batch and head_dim')
+    kv_heads = new_key.shape[2]
+    if (key_arena.ndim != 4 or key_arena.shape != value_arena.shape or key_arena.shape[0] < batch
+            or key_arena.shape[1] != kv_heads or key_arena.shape[3] != head_dim
+            or not key_arena.is_contiguous() or not value_arena.is_contiguous()):
+        raise ValueError('arena planes must be contiguous (slots, kv_heads, capacity, head_dim)')
+    if head_dim != 128 or q_heads % kv_heads:
+        raise ValueError('fused decode supports head_dim 128 with q_heads a multiple of kv_heads')
+    tensors = (query, new_key, new_value, key_arena, value_arena, cos, sin)
+    if any(t.dtype != torch.bfloat16 for t in tensors):
+        raise ValueError('fused decode is bf16-only (exact RoPE rounding contract)')
+    if positions.shape != (batch,) or positions.dtype != torch.int64:
+        raise ValueError('positions must be an int64 (batch,) tensor')
+    cos2 = cos.reshape(cos.shape[0], -1) if cos.ndim == 3 else cos
+    sin2 = sin.reshape(sin.shape[0], -1) if sin.ndim == 3 else sin
+    if cos2.shape != (batch, head_dim) or sin2.shape != cos2.shape or cos2.stride(1) != 1 or sin2.stride() != cos2.stride():
+        raise ValueError('cos/sin must be (B, head_dim) rows')
+    if any(t.stride(3) != 1 for t in (query, new_key, new_value)):
+        raise ValueError('rows must be unit-stride along head_dim')
+    device = _lib.require_gpu(*tensors, positions)
+    if out is None:
+        out = torch.empty(batch, 1, q_heads, head_dim, device=device, dtype=query.dtype)
+    a = _lib.DecodeArgs()
+    a.batch, a.query_len, a.q_heads, a.kv_heads, a.head_dim = batch, 1, q_heads, kv_heads, head_dim
+    a.ctx = key_arena.shape[2]
+    a.dtype = _lib.Q3T_BF16
+    a.scale = head_dim ** -0.5 if scale is None else float(scale)
+    a.fused = 1
+    a.query = query.data_ptr()
+    a.q_stride_b, a.q_stride_s, a.q_stride_h = query.stride()[:3]
+    a.keys, a.values = key_arena.data_ptr(), value_arena.data_ptr()
+    a.k_stride_b, a.k_stride_h, a.k_stride_t = key_arena.stride()[:3]
+    a.v_stride_b, a.v_stride_h, a.v_stride_t = value_arena.stride()[:3]
+    a.positions = positions.data_ptr()
+    a.out = out.data_ptr()
+    a.o_stride_b, a.o_stride_s, a.o_stride_h = out.stride()[:3]
+    a.new_key, a.new_value = new_key.data_ptr(), new_value.data_ptr()
+    a.nk_stride_b, a.nk_stride_h = new_key.stride(0), new_key.stride(2)
+    a.nv_stride_b, a.nv_stride_h = new_value.stride(0), new_value.stride(2)
+    a.cos, a.sin = cos2.data_ptr(), sin2.data_ptr()
+    a.cs_stride_b = cos2.stride(0)
+    a.splits_per_head = int(splits_per_head or 0)
+    _run_decode(a, device, 'fused decode step')
+    return out
+
+
+def attention(module, query, key, value, attention_mask, **kwargs):
+    """Drop-in for the reference's native GQA call: query (B, Hq, S, D), key/value
+    (B, Hkv, ctx, D) BNSD; returns ((B, S, Hq, D) contiguous, None).
+
+    ``kv_positions`` (a device int64 (B,) tensor, as kept by SlotCache) limits request b to
+    keys 0 ... kv_positions[b]; ``actual_seq_lengths_kv`` (list of ints) limits it to that
+    many keys; the mask, if any, is applied on top, as the reference's operator does."""
+    if module.training or kwargs.get('dropout', 0.0) != 0.0:
+        raise ValueError('Native GQA is inference-only')
+    if getattr(module, 'sliding_window', None) is not None:
+        raise ValueError('Native GQA sliding-window masks are not implemented')
+    batch, _, qlen, head_dim = query.shape
+    ctx = key.shape[2]
+    scale = kwargs.get('scaling', head_dim ** -0.5)
+    positions = kwargs.get('kv_positions')
+    lengths = kwargs.get('actual_seq_lengths_kv')
+    device = query.device
+    if positions is None:
+        if lengths is not None:
+            positions = torch.tensor([int(n) - 1 for n in lengths], device=device, dtype=torch.int64)
+        else:
+            positions = torch.full((batch,), ctx - 1, device=device, dtype=torch.int64)
+    mask = attention_mask
+    if mask is not None and qlen > 2:
+        raise ValueError('explicit masks are supported for query lengths up to 2; '
+                         'use prefill_attention for causal prefill')
+    if qlen <= 2:
+        out = decode_attention(query.transpose(1, 2), key, value, positions, scale=scale, mask=mask)
+        return out, None
+    if not getattr(module, 'is_causal', True):
+        raise ValueError('non-causal prefill without a mask is not supported')
+    # causal prefill of equal-length rows: request b's queries sit at positions 0 ... qlen-1
+    cu = torch.arange(0, (batch + 1) * qlen, qlen, device=device, dtype=torch.int32)
+    q = query.transpose(1, 2).reshape(batch * qlen, query.shape[1], head_dim)
+    out = prefill_attention(q, key, value, cu, qlen, scale=scale)
+    return out.view(batch, qlen, query.shape[1], head_dim), None
+
+
+def prefill_attention(query, keys, values, cu_seqlens, max_seqlen, *, scale=None, kv_slots=None,
+                      out=None):
+    """Varlen causal GQA: query (T, Hq, D) packed by cu_seqlens (B+1, int32); keys/values
+    (slots, Hkv, capacity, D) arena views holding each request's keys at positions
+    0 ... len-1 (slot b, or kv_slots[b]).  Returns (T, Hq, D)."""
+    if query.ndim != 3 or keys.ndim != 4 or values.shape != keys.shape:
+        raise ValueError('expected (T, Hq, D) queries and arena key/value views')
+    total, q_heads, head_dim = query.shape
+    kv_heads = keys.shape[1]
+    if query.dtype != torch.bfloat16 or keys.dtype != torch.bfloat16 or values.dtype != torch.bfloat16:
+        raise ValueError('prefill attention is bf16-only')
+    if cu_seqlens.dtype != torch.int32 or cu_seqlens.ndim != 1 or cu_seqlens.numel() < 2:
+        raise ValueError('cu_seqlens must be an int32 (B+1,) tensor')
+    if keys.shape[3] != head_dim or q_heads % kv_heads:
+        raise ValueError('head_dim mismatch or q_heads not a multiple of kv_heads')
+    if query.stride(2) != 1 or keys.stride(3) != 1 or values.stride(3) != 1:
+        raise ValueError('rows must be unit-stride along head_dim')
+    device = _lib.require_gpu(query, keys, values, cu_seqlens)
+    batch = cu_seqlens.numel() - 1
+    if out is None:
+        out = torch.empty(total, q_heads, head_dim, device=device, dtype=query.dtype)
+    a = _lib.PrefillArgs()
+    a.batch, a.total_tokens, a.max_seqlen = batch, total, int(max_seqlen)
+    a.q_heads, a.kv_heads, a.head_dim = q_heads, kv_heads, head_dim
+    a.scale = head_dim ** -0.5 if scale is None else float(scale)
+    a.cu_seqlens = cu_seqlens.data_ptr()
+    a.query = query.data_ptr()
+    a.q_stride_t, a.q_stride_h = query.stride()[:2]
+    a.keys, a.values = keys.data_ptr(), values.data_ptr()
+    a.k_stride_b, a.k_stride_h, a.k_stride_t = keys.stride()[:3]
+    a.v_stride_b, a.v_stride_h, a.v_stride_t = values.stride()[:3]
+    if kv_slots is not None:
+        if kv_slots.dtype != torch.int64 or kv_slots.shape != (batch,):
+            raise ValueError('kv_slots must be an int64 (B,) tensor')
+        a.kv_slots = kv_slots.data_ptr()
+    a.out = out.data_ptr()
+    a.o_stride_t, a.o_stride_h = out.stride()[:2]
+    status = _lib.library().q3t_prefill_attention(a, _lib.stream_handle(device))
+    _lib.check(status, 'prefill attention')
+    return out

@@ -1,0 +1,102 @@
+// Shared device helpers for the gfx950 kernels: bf16 bit conversions with torch's
+// rounding, DPP lane reductions and 16-byte vector access.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/qwen3tts_amd.h"
+
+#define Q3T_DEVICE __device__ __forceinline__
+
+namespace q3t {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// bf16 (as raw 16 bits) -> fp32: exact.
+Q3T_DEVICE float bf16_to_float(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+Q3T_DEVICE float bf16_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
+Q3T_DEVICE float bf16_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u); }
+
+// fp32 -> bf16 bits, round-to-nearest-even; NaN maps to 0x7fc0 as c10::BFloat16 does.
+Q3T_DEVICE uint32_t float_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+// Round through bf16 and back (one torch-eager bf16 op boundary).
+Q3T_DEVICE float round_bf16(float f) { return bf16_to_float(float_to_bf16(f)); }
+
+Q3T_DEVICE uint32_t pack_bf16(float lo, float hi) {
+    return float_to_bf16(lo) | (float_to_bf16(hi) << 16);
+}
+
+// a.lo*b.lo + a.hi*b.hi + c on packed bf16 pairs (v_dot2c_f32_bf16).
+Q3T_DEVICE float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                           __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// DPP lane exchanges within rows of 16 lanes.
+template <int CTRL>
+Q3T_DEVICE float dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i within each 8-lane half row
+
+// Sum over each aligned group of 8 lanes; every lane of the group receives the total.
+Q3T_DEVICE float sum8(float x) {
+    x += dpp<kDppXor1>(x);
+    x += dpp<kDppXor2>(x);
+    x += dpp<kDppHalfMirror>(x);
+    return x;
+}
+
+struct alignas(16) U4 { uint32_t x, y, z, w; };
+
+Q3T_DEVICE U4 load16(const void *p) { return *reinterpret_cast<const U4 *>(p); }
+Q3T_DEVICE void store16(void *p, U4 v) { *reinterpret_cast<U4 *>(p) = v; }
+
+// Rotate-half RoPE on one packed bf16 pair of the first half (x1) and the matching pair of
+// the second half (x2), reproducing torch-eager bf16 rounding after every op
+// (reference contract: rotary_triton_ascend.py:19-24):
+//   y1 = bf16(bf16(x1*c1) + bf16(-x2*s1)),  y2 = bf16(bf16(x2*c2) + bf16(x1*s2)).
+// Products of two bf16 values are exact in fp32; each sum rounds to fp32 and then to bf16,
+// the same double rounding torch performs for a bf16 add.
+Q3T_DEVICE void rope_pair(uint32_t x1, uint32_t x2, uint32_t c1, uint32_t c2, uint32_t s1,
+                          uint32_t s2, uint32_t &y1, uint32_t &y2) {
+    float a[2] = {bf16_lo(x1), bf16_hi(x1)}, b[2] = {bf16_lo(x2), bf16_hi(x2)};
+    float cc1[2] = {bf16_lo(c1), bf16_hi(c1)}, cc2[2] = {bf16_lo(c2), bf16_hi(c2)};
+    float ss1[2] = {bf16_lo(s1), bf16_hi(s1)}, ss2[2] = {bf16_lo(s2), bf16_hi(s2)};
+    uint32_t o1[2], o2[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        float left = round_bf16(a[e] * cc1[e]);
+        float right = round_bf16(-(b[e] * ss1[e]));
+        o1[e] = float_to_bf16(left + right);
+        float left2 = round_bf16(b[e] * cc2[e]);
+        float right2 = round_bf16(a[e] * ss2[e]);
+        o2[e] = float_to_bf16(left2 + right2);
+    }
+    y1 = o1[0] | (o1[1] << 16);
+    y2 = o2[0] | (o2[1] << 16);
+}
+
+// RoPE on 8 consecutive dims of each half (one 16-byte vector per half).
+Q3T_DEVICE void rope8(const uint32_t *x1, const uint32_t *x2, const uint32_t *c1, const uint32_t *c2,
+                      const uint32_t *s1, const uint32_t *s2, uint32_t *y1, uint32_t *y2) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rope_pair(x1[i], x2[i], c1[i], c2[i], s1[i], s2[i], y1[i], y2[i]);
+}
+
+inline bool aligned(const void *p, int64_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+inline int launch_status() {
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? Q3T_OK : static_cast<int>(e);
+}
+
+}  // namespace q3t

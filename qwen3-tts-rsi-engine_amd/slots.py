@@ -1,0 +1,143 @@
+"""KV state of continuous batching: slot arena, slot cache, predictor cache.
+
+Drop-ins for the reference's ``SlotArena`` / ``SlotCache`` (qwen3_tts_engine/continuous.py:97-169)
+and ``PredictorCache`` (qwen3_tts_engine/predictor.py:9-27): same constructors, attributes and
+``update`` contract.  Every device-side byte move (decode K/V write, prefix load, slot
+compaction, capacity regrowth) is a HIP kernel of this package.
+"""
+from __future__ import annotations
+
+import torch
+from transformers.cache_utils import Cache
+
+from . import kv_write
+from .packed_kv import copy_packed_prefix, copy_rows
+
+
+class SlotArena:
+    """Per-slot KV storage for every talker layer.
+
+    ``packed_kv=True`` keeps all layers in one (2*layers, slots, kv_heads, capacity, head_dim)
+    tensor (keys first), as continuous.py:109-113 does; otherwise one tensor per layer."""
+
+    def __init__(self, reference, slots, capacity, native_kv_update=False, triton_kv_update=False,
+                 packed_kv=False):
+        self.reference = reference
+        self.slots = slots
+        self.capacity = capacity
+        self.native_kv_update = native_kv_update
+        self.triton_kv_update = triton_kv_update
+        self.packed_kv = packed_kv
+        weight = next(reference.parameters())
+        config = reference.config
+        shape = (slots, config.num_key_value_heads, capacity, config.head_dim)
+        self.packed = None
+        if packed_kv:
+            layers = len(reference.layers)
+            self.packed = torch.zeros((layers * 2, *shape), device=weight.device, dtype=weight.dtype)
+            self.keys = list(self.packed[:layers].unbind(0))
+            self.values = list(self.packed[layers:].unbind(0))
+        else:
+            self.keys = [torch.zeros(shape, device=weight.device, dtype=weight.dtype)
+                         for _ in reference.layers]
+            self.values = [torch.zeros_like(key) for key in self.keys]
+
+    def load(self, slot, cache, row=0, length=None):
+        """Copy the first ``length`` positions of one prefill cache row into ``slot``."""
+        length = cache.get_seq_length() if length is None else length
+        for i, layer in enumerate(cache.layers):
+            copy_rows(self.keys[i][slot, :, :length], layer.keys[row, :, :length])
+            copy_rows(self.values[i][slot, :, :length], layer.values[row, :, :length])
+
+    def move(self, source, destination):
+        """Compaction: the whole slot row ``source`` overwrites ``destination`` in every layer."""
+        if source == destination:
+            return
+        if self.packed is not None:
+            copy_rows(self.packed[:, destination], self.packed[:, source])
+            return
+        for keys, values in zip(self.keys, self.values):
+            copy_rows(keys[destination], keys[source])
+            copy_rows(values[destination], values[source])
+
+    def load_packed(self, slot, cache, row=0, length=None):
+        copy_packed_prefix(self.packed, cache, slot, row=row, length=length)
+
+    def planes(self):
+        """Every key plane followed by every value plane (the packed order)."""
+        return self.keys + self.values
+
+
+def grow_arena(old: SlotArena, required: int) -> SlotArena:
+    """A larger arena holding ``old``'s contents, with the reference's capacity rule
+    max(2*C, 2**bit_length(required)) (continuous.py:353-363).  ``required < C`` returns ``old``."""
+    if required < old.capacity:
+        return old
+    capacity = max(old.capacity * 2, 1 << int(required).bit_length())
+    new = SlotArena(old.reference, old.slots, capacity, old.native_kv_update, old.triton_kv_update,
+                    packed_kv=old.packed_kv)
+    if new.packed is not None:
+        copy_rows(new.packed[:, :, :, :old.capacity], old.packed)
+    else:
+        for target, source in zip(new.planes(), old.planes()):
+            copy_rows(target[:, :, :old.capacity], source)
+    return new
+
+
+class SlotCache(Cache):
+    """HF ``Cache`` whose ``update`` writes one decode token per request into the arena at
+    ``positions[b]`` and returns the arena views the attention reads."""
+
+    def __init__(self, arena, positions, context_length=None, valid_length_kv=False):
+        super().__init__(layers=[])
+        self.arena = arena
+        self.positions = positions
+        self.context_length = arena.capacity if context_length is None else context_length
+        self.actual_seq_lengths_kv = ([self.context_length] * positions.shape[0]
+                                      if valid_length_kv else None)
+
+    def prepare(self):
+        """Index preparation hook of the reference; the HIP writer reads positions directly."""
+
+    def update(self, keys, values, layer_idx, cache_kwargs):
+        batch = keys.shape[0]
+        target_keys = self.arena.keys[layer_idx][:batch]
+        target_values = self.arena.values[layer_idx][:batch]
+        kv_write.write(keys, values, target_keys, target_values, self.positions)
+        if self.actual_seq_lengths_kv is not None:
+            return target_keys, target_values
+        return (target_keys[:, :, :self.context_length],
+                target_values[:, :, :self.context_length])
+
+
+class PredictorCache(Cache):
+    """Fixed 16-position cache of the code predictor: step 0 writes positions [0, 2),
+    step s >= 1 writes position s + 1; ``update`` returns the [:step + 2] views."""
+
+    def __init__(self, reference, inputs, capacity=16):
+        super().__init__(layers=[])
+        config = reference.config
+        shape = (inputs.shape[0], config.num_key_value_heads, capacity, config.head_dim)
+        self.keys = [torch.zeros(shape, device=inputs.device, dtype=inputs.dtype)
+                     for _ in range(config.num_hidden_layers)]
+        self.values = [torch.zeros_like(tensor) for tensor in self.keys]
+        self.step = 0
+        self._starts = {}
+
+    def _start_positions(self, batch, start, device):
+        key = (batch, start, device)
+        if key not in self._starts:  # constant per (batch, step): kept alive for graph replays
+            self._starts[key] = torch.full((batch,), start, device=device, dtype=torch.int64)
+        return self._starts[key]
+
+    def update(self, keys, values, layer_index, cache_kwargs):
+        start = 0 if self.step == 0 else self.step + 1
+        end = self.step + 2
+        if keys.shape[2] != end - start:
+            raise ValueError('predictor step writes one token (two at step 0)')
+        positions = self._start_positions(keys.shape[0], start, keys.device)
+        kv_write.write_tokens(keys, values, self.keys[layer_index], self.values[layer_index], positions)
+        return self.keys[layer_index][:, :, :end], self.values[layer_index][:, :, :end]
+
+    def get_seq_length(self, layer_idx=0):
+        return 0 if self.step == 0 else self.step + 1

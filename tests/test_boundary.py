@@ -1,0 +1,114 @@
+"""The C-ABI boundary without a GPU: the library loads, exports every symbol the header
+declares, its structs match ctypes field for field, and host validation raises ValueError
+before anything is launched (the reference's error convention, tests/test_packed_kv.py:45-81)."""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "qwen3tts_amd.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    names = re.findall(r"\b(q3t_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    lib = pkg.library()
+    names = declared_functions()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+    assert set(names) == set(pkg._lib.SIGNATURES), "ctypes signatures out of sync with the header"
+
+
+def test_status_strings_and_version(pkg):
+    lib = pkg.library()
+    assert lib.q3t_abi_version() == 1
+    assert lib.q3t_status_string(0) == b"success"
+    assert lib.q3t_status_string(-1) == b"invalid argument"
+    assert lib.q3t_status_string(-3) == b"workspace missing or too small"
+
+
+def _c_layout(struct_name, fields, tmp_path):
+    src = tmp_path / "layout.c"
+    lines = [f'#include "{HEADER}"', "#include <stdio.h>", "#include <stddef.h>", "int main(void) {",
+             f'  printf("%zu\\n", sizeof({struct_name}));']
+    lines += [f'  printf("%zu\\n", offsetof({struct_name}, {f}));' for f in fields]
+    lines += ["  return 0;", "}"]
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", str(src), "-o", str(exe)], check=True)
+    return [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+
+
+@pytest.mark.parametrize("name,cls", [("q3t_decode_args", "DecodeArgs"), ("q3t_prefill_args", "PrefillArgs"),
+                                      ("q3t_prefill_rope_write_args", "PrefillRopeWriteArgs")])
+def test_struct_layouts_match_the_header(pkg, tmp_path, name, cls):
+    struct = getattr(pkg._lib, cls)
+    fields = [f for f, _ in struct._fields_]
+    c = _c_layout(name, fields, tmp_path)
+    assert c[0] == ctypes.sizeof(struct)
+    assert c[1:] == [getattr(struct, f).offset for f in fields]
+
+
+def test_rejected_calls_return_negative_status_without_a_gpu(pkg):
+    lib = pkg.library()
+    zero = pkg._lib.i64x3((0, 0, 0))
+    assert lib.q3t_kv_write(None, None, None, None, None, 1, 1, 1, 1, 2, zero, zero, zero, 1, None) == -1
+    assert lib.q3t_rotary(None, None, None, None, 1, 1, 128, 0, None) == -1
+    assert lib.q3t_decode_attention(None, None) == -1
+    args = pkg._lib.DecodeArgs()
+    args.batch, args.query_len, args.q_heads, args.kv_heads, args.head_dim, args.ctx = 1, 1, 16, 8, 96, 8
+    args.query = args.keys = args.values = args.positions = args.out = 16
+    args.dtype = 0
+    assert lib.q3t_decode_attention(args, None) == -2   # head_dim 96 not compiled
+    args.head_dim, args.splits_per_head = 128, 4
+    assert lib.q3t_decode_attention(args, None) == -3   # no workspace
+    assert lib.q3t_decode_workspace_bytes(64, 1, 16, 8, 128, 64) == 65536 * 4 + 8 * 64 * 2 * 2 * 130 * 4
+
+
+def test_wrappers_reject_cpu_tensors(pkg):
+    k = torch.zeros(2, 8, 1, 128, dtype=torch.bfloat16)
+    t = torch.zeros(2, 8, 16, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        pkg.write(k, k, t, t.clone(), torch.zeros(2, dtype=torch.int64))
+    with pytest.raises(ValueError):
+        pkg.rotary(torch.zeros(1, 1, 8, 128, dtype=torch.bfloat16), torch.zeros(1, 1, 128, dtype=torch.bfloat16),
+                   torch.zeros(1, 1, 128, dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        pkg.decode_attention(torch.zeros(2, 1, 16, 128, dtype=torch.bfloat16), t, t,
+                             torch.zeros(2, dtype=torch.int64))
+
+
+def test_kv_write_validation_mirrors_reference(pkg):
+    """kv_triton_ascend.write's shape/dtype/position checks (kv_triton_ascend.py:41-53)."""
+    k = torch.zeros(2, 8, 1, 128, dtype=torch.bfloat16)
+    t = torch.zeros(2, 8, 16, 128, dtype=torch.bfloat16)
+    pos = torch.zeros(2, dtype=torch.int64)
+    for bad in [(k[:, :, :0], k, t, t, pos), (k, k, t[:1], t[:1], pos), (k, k, t, t, pos.int()),
+                (k, k, t, t, pos[:1]), (k, k.float(), t, t, pos), (k, k, t[..., ::2], t[..., ::2], pos)]:
+        with pytest.raises(ValueError):
+            pkg.write(*bad)
+
+
+def test_packed_prefix_rejects_before_any_write(pkg):
+    """tests/test_packed_kv.py:45-81 run on CPU tensors: every invalid call raises."""
+    target = torch.full((4, 5, 2, 7, 3), -7.0)
+    source = torch.arange(4 * 3 * 2 * 5 * 6).view(4, 3, 2, 5, 6).float()[..., ::2]
+    saved = target.clone()
+    for slot, row, length in ((-1, 0, 1), (5, 0, 1), (0, 3, 1), (0, -1, 1), (0, 0, 0), (0, 0, 6),
+                              (True, 0, 1), (0, True, 1), (0, 0, True)):
+        with pytest.raises(ValueError):
+            pkg.copy_packed_prefix(target, source, slot, row=row, length=length)
+    for bad in (source[:3], source[:, :, :1], source[..., :2], source.double(), source[0], source[:, :0],
+                target, torch.empty_like(source, device="meta")):
+        with pytest.raises(ValueError):
+            pkg.copy_packed_prefix(target, bad, 0, length=1)
+    assert torch.equal(target, saved)

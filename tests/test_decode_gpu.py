@@ -1,0 +1,284 @@
+"""Ragged GQA decode attention on the GPU against the float64 oracle.
+
+Configs follow the build's workloads: config 1 (fp32 CPU-plumbing case, contexts
+{37, 120, 5, 256}), config 2 (64-request ragged talker step, contexts U[64, 1024], seed 0),
+and the code predictor's 16-slot cache (query length 2 at step 0).  Tolerance for bf16 I/O
+with fp32 accumulation: max-abs <= 2e-2 and mean-abs <= 2e-3; fp32 I/O: 1e-5."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oatt
+from oracle import bf16 as obf16
+from oracle import kv as okv
+from oracle import rope as orope
+from tests._util import assert_attention_close, bits, f64
+
+pytestmark = pytest.mark.gpu
+
+HQ, HKV, D = 16, 8, 128
+
+
+def _arena(batch, capacity, dtype, device, seed, kv_heads=HKV, head_dim=D):
+    gen = torch.Generator(device=device).manual_seed(seed)
+    k = torch.randn(batch, kv_heads, capacity, head_dim, generator=gen, device=device, dtype=dtype)
+    v = torch.randn(batch, kv_heads, capacity, head_dim, generator=gen, device=device, dtype=dtype)
+    return k, v
+
+
+def test_config1_fp32_write_rope_attention(pkg, device):
+    """4 requests, contexts {37,120,5,256}, fp32: RoPE at position c_b, write at c_b,
+    attend L_b = c_b + 1 keys."""
+    contexts = [37, 120, 5, 256]
+    batch, capacity = 4, 257
+    gen = torch.Generator().manual_seed(0)
+    cache_k = torch.zeros(batch, HKV, capacity, D)
+    cache_v = torch.zeros(batch, HKV, capacity, D)
+    for b, c in enumerate(contexts):
+        cache_k[b, :, :c] = torch.randn(HKV, c, D, generator=gen)
+        cache_v[b, :, :c] = torch.randn(HKV, c, D, generator=gen)
+    q = torch.randn(batch, 1, HQ, D, generator=gen)
+    k = torch.randn(batch, 1, HKV, D, generator=gen)
+    v = torch.randn(batch, 1, HKV, D, generator=gen)
+    positions = torch.tensor(contexts)
+    inv = pkg.inverse_frequencies(D)
+    cos, sin = pkg.rope_tables(positions.to(device)[:, None], D, dtype=torch.float32)
+    q_rot = pkg.rotary(q.to(device), cos, sin)
+    k_rot = pkg.rotary(k.to(device), cos, sin)
+    dk, dv = cache_k.to(device), cache_v.to(device)
+    pkg.write(k_rot.transpose(1, 2), v.to(device).transpose(1, 2), dk, dv, positions.to(device))
+    out = pkg.decode_attention(q_rot, dk, dv, positions.to(device))
+    # oracle chain
+    ocos, osin = orope.tables(positions.numpy()[:, None], inv.numpy(), dtype="f32")
+    np.testing.assert_allclose(cos.cpu().numpy(), ocos, atol=2.5e-7, rtol=0)
+    c_np, s_np = cos.cpu().numpy()[:, :, None, :], sin.cpu().numpy()[:, :, None, :]
+    eq = orope.rope_f32(q.numpy(), c_np, s_np)
+    ek_rot = orope.rope_f32(k.numpy(), c_np, s_np)
+    assert np.array_equal(q_rot.cpu().numpy(), eq) and np.array_equal(k_rot.cpu().numpy(), ek_rot)
+    ek, ev = okv.kv_write(cache_k.numpy().copy(), cache_v.numpy().copy(),
+                          ek_rot.transpose(0, 2, 1, 3), v.numpy().transpose(0, 2, 1, 3), contexts)
+    assert np.array_equal(dk.cpu().numpy(), ek) and np.array_equal(dv.cpu().numpy(), ev)
+    expected = oatt.decode_attention(eq, ek, ev, contexts, D ** -0.5)
+    np.testing.assert_allclose(f64(out), expected, atol=1e-5, rtol=0)
+
+
+def _config2(device, capacity=1024, seed=0):
+    gen = torch.Generator().manual_seed(seed)
+    contexts = torch.randint(64, 1025, (64,), generator=gen)
+    k, v = _arena(64, capacity, torch.bfloat16, device, seed + 1)
+    qkv = torch.randn(64, 1, (HQ + 2 * HKV) * D, generator=gen).bfloat16().to(device)
+    q = qkv[..., :HQ * D].view(64, 1, HQ, D)
+    kn = qkv[..., HQ * D:(HQ + HKV) * D].view(64, 1, HKV, D)
+    vn = qkv[..., (HQ + HKV) * D:].view(64, 1, HKV, D)
+    return contexts, k, v, q, kn, vn
+
+
+def _expected_fused(contexts, k, v, q, kn, vn, cos, sin):
+    cb, sb = bits(cos)[:, None, None, :], bits(sin)[:, None, None, :]
+    q_rot = orope.rope_bf16(bits(q), cb, sb)
+    k_rot = orope.rope_bf16(bits(kn), cb, sb)
+    ak, av = okv.kv_write(bits(k).copy(), bits(v).copy(), k_rot.transpose(0, 2, 1, 3),
+                          bits(vn).transpose(0, 2, 1, 3), contexts.numpy())
+    out = oatt.decode_attention(obf16.from_bits(q_rot), obf16.from_bits(ak), obf16.from_bits(av),
+                                contexts.numpy(), D ** -0.5)
+    return ak, av, out
+
+
+@pytest.mark.parametrize("splits", [0, 1, 7, 64, 3000])
+def test_config2_fused_decode_step(pkg, device, splits):
+    """The headline step: RoPE + write + ragged GQA over 64 requests, seed 0 (sum c = 32718)."""
+    contexts, k, v, q, kn, vn = _config2(device)
+    assert int(contexts.sum()) == 32718
+    positions = contexts.to(device)
+    cos, sin = pkg.rope_tables(positions, D)
+    expected_k, expected_v, expected = _expected_fused(contexts, k, v, q, kn, vn, cos, sin)
+    out = pkg.decode_step(q, kn, vn, k, v, positions, cos, sin, splits_per_head=splits)
+    assert np.array_equal(bits(k), expected_k) and np.array_equal(bits(v), expected_v)
+    assert_attention_close(f64(out)[:, 0], expected[:, 0])
+
+
+def test_fused_matches_unfused_chain(pkg, device):
+    """rotary -> write -> decode_attention gives the same output as the fused launch."""
+    contexts, k, v, q, kn, vn = _config2(device, seed=3)
+    positions = contexts.to(device)
+    cos, sin = pkg.rope_tables(positions, D)
+    k2, v2 = k.clone(), v.clone()
+    fused = pkg.decode_step(q, kn, vn, k, v, positions, cos, sin)
+    q_rot = pkg.rotary(q.contiguous(), cos[:, None], sin[:, None])
+    k_rot = pkg.rotary(kn.contiguous(), cos[:, None], sin[:, None])
+    pkg.write(k_rot.transpose(1, 2), vn.transpose(1, 2), k2, v2, positions)
+    chain = pkg.decode_attention(q_rot, k2, v2, positions)
+    assert torch.equal(k, k2) and torch.equal(v, v2)
+    diff = (fused.float() - chain.float()).abs()
+    assert diff.max().item() <= 1e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("group", [1, 2, 4])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("qlen", [1, 2])
+def test_decode_shapes(pkg, device, dtype, group, head_dim, qlen):
+    kv_heads, batch, capacity = 4, 9, 300
+    gen = torch.Generator().manual_seed(group * 100 + head_dim + qlen)
+    lengths = torch.tensor([1, 2, 3, 17, 64, 65, 128, 255, 300])[:batch]
+    positions = lengths - 1
+    if qlen == 2:
+        positions = positions.clamp(min=1)
+    k, v = _arena(batch, capacity, dtype, device, 11, kv_heads=kv_heads, head_dim=head_dim)
+    q = torch.randn(batch, qlen, kv_heads * group, head_dim, generator=gen).to(dtype).to(device)
+    out = pkg.decode_attention(q, k, v, positions.to(device))
+    expected = oatt.decode_attention(f64(q), f64(k), f64(v), positions.numpy(), head_dim ** -0.5)
+    if dtype == torch.float32:
+        np.testing.assert_allclose(f64(out), expected, atol=1e-5, rtol=0)
+    else:
+        assert_attention_close(f64(out), expected)
+
+
+def test_poisoned_tail_is_never_read(pkg, device):
+    """Keys beyond pos[b] hold stale or garbage data (tools/probe_attention_context.py:53-55):
+    inf/NaN there must not leak into the output."""
+    contexts, k, v, q, _, _ = _config2(device, seed=5)
+    positions = contexts.to(device)
+    mask = torch.arange(1024, device=device)[None, :] > positions[:, None]
+    clean = pkg.decode_attention(q, k, v, positions).clone()
+    k.masked_fill_(mask[:, None, :, None], float('inf'))
+    v.masked_fill_(mask[:, None, :, None], float('nan'))
+    poisoned = pkg.decode_attention(q, k, v, positions)
+    assert torch.equal(clean, poisoned)
+
+
+@pytest.mark.parametrize("kind", ["additive_bf16", "additive_f32", "bool"])
+def test_mask_matches_sdpa_semantics(pkg, device, kind):
+    """SlotGraph's additive mask (0 / finfo.min for j <= pos, continuous.py:191-192) over the
+    whole arena equals the position-limited attention; an arbitrary mask follows SDPA."""
+    batch, capacity = 8, 256
+    k, v = _arena(batch, capacity, torch.bfloat16, device, 21)
+    gen = torch.Generator().manual_seed(22)
+    q = torch.randn(batch, 1, HQ, D, generator=gen).bfloat16().to(device)
+    allowed = torch.rand(batch, 1, capacity, generator=gen) < 0.6
+    allowed[:, :, 0] = True
+    if kind == "bool":
+        mask = allowed
+    else:
+        dtype = torch.bfloat16 if kind == "additive_bf16" else torch.float32
+        mask = torch.where(allowed, 0.0, torch.finfo(dtype).min).to(dtype)
+    full = torch.full((batch,), capacity - 1, dtype=torch.int64, device=device)
+    out = pkg.decode_attention(q, k, v, full, mask=mask[:, None].to(device))
+    expected = oatt.decode_attention(f64(q), f64(k), f64(v), full.cpu().numpy(), D ** -0.5,
+                                     mask=allowed.numpy())
+    assert_attention_close(f64(out), expected)
+
+
+def test_trimmed_context_equals_masked_arena(pkg, device):
+    """tests/test_slot_context.py:32-36: attention over the trimmed context equals
+    attention over the full arena under the j <= pos mask."""
+    batch, capacity = 2, 256
+    k, v = _arena(batch, capacity, torch.float32, device, 42, kv_heads=2, head_dim=64)
+    gen = torch.Generator().manual_seed(42)
+    q = torch.randn(batch, 1, 2, 64, generator=gen).to(device)
+    for context, pos in ((64, [63, 17]), (128, [64, 127])):
+        positions = torch.tensor(pos, device=device)
+        mask = torch.arange(capacity, device=device)[None, :] <= positions[:, None]
+        full = pkg.decode_attention(q, k, v, torch.full_like(positions, capacity - 1),
+                                    mask=mask[:, None, None])
+        trimmed = pkg.decode_attention(q, k[:, :, :context], v[:, :, :context], positions)
+        torch.testing.assert_close(trimmed, full, atol=1e-6, rtol=1e-6)
+
+
+def test_predictor_windows_qlen2_then_single(pkg, device):
+    """Code predictor: step 0 attends a 2x2 causal window, step s attends [:s + 2] of a
+    16-slot cache (continuous.py:37-40, predictor.py:19-24); batch 64."""
+    k, v = _arena(64, 16, torch.bfloat16, device, 31)
+    gen = torch.Generator().manual_seed(32)
+    for step in range(15):
+        qlen = 2 if step == 0 else 1
+        q = torch.randn(64, qlen, HQ, D, generator=gen).bfloat16().to(device)
+        positions = torch.full((64,), step + 1, dtype=torch.int64, device=device)
+        out = pkg.decode_attention(q, k, v, positions)
+        expected = oatt.decode_attention(f64(q), f64(k), f64(v), positions.cpu().numpy(), D ** -0.5)
+        assert_attention_close(f64(out), expected)
+    # the reference's explicit 2x2 mask (finfo.min above the diagonal) gives the same result
+    q = torch.randn(64, 2, HQ, D, generator=gen).bfloat16().to(device)
+    mask = torch.zeros(1, 1, 2, 2, dtype=torch.bfloat16)
+    mask[..., 0, 1] = torch.finfo(torch.bfloat16).min
+    positions = torch.ones(64, dtype=torch.int64, device=device)
+    with_mask = pkg.decode_attention(q, k[:, :, :2], v[:, :, :2], positions, mask=mask.to(device))
+    implicit = pkg.decode_attention(q, k[:, :, :2], v[:, :, :2], positions)
+    assert torch.equal(with_mask, implicit)
+
+
+def test_invalid_positions_write_nothing_and_output_zero(pkg, device):
+    batch, capacity = 4, 64
+    k, v = _arena(batch, capacity, torch.bfloat16, device, 41)
+    gen = torch.Generator().manual_seed(42)
+    qkv = torch.randn(batch, 1, (HQ + 2 * HKV) * D, generator=gen).bfloat16().to(device)
+    q = qkv[..., :HQ * D].view(batch, 1, HQ, D)
+    kn = qkv[..., HQ * D:(HQ + HKV) * D].view(batch, 1, HKV, D)
+    vn = qkv[..., (HQ + HKV) * D:].view(batch, 1, HKV, D)
+    positions = torch.tensor([5, 64, -1, 63], device=device)
+    cos, sin = pkg.rope_tables(positions.clamp(min=0), D)
+    before_k, before_v = k.clone(), v.clone()
+    out = pkg.decode_step(q, kn, vn, k, v, positions, cos, sin)
+    assert torch.equal(k[1:3], before_k[1:3]) and torch.equal(v[1:3], before_v[1:3])
+    assert not out[1:3].any()
+    assert out[0].abs().sum() > 0 and out[3].abs().sum() > 0
+
+
+def test_graph_replay_with_changing_positions(pkg, device):
+    """A captured fused step replayed while positions advance and inputs change in place
+    (the SlotGraph.run pattern, continuous.py:218-224): every replay matches the oracle."""
+    contexts, k, v, q, kn, vn = _config2(device, seed=7)
+    qkv = q.as_strided((64, 1, (HQ + 2 * HKV) * D), (q.stride(0), q.stride(1), 1))
+    positions = contexts.to(device).clone()
+    cos, sin = pkg.rope_tables(positions, D)
+    out = pkg.decode_step(q, kn, vn, k, v, positions, cos, sin)  # eager: sizes the workspace
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = pkg.decode_step(q, kn, vn, k, v, positions, cos, sin)
+    gen = torch.Generator().manual_seed(8)
+    host_pos = contexts.clone()
+    for replay in range(3):
+        host_pos += 1
+        positions.copy_(host_pos.to(device))
+        c2, s2 = pkg.rope_tables(positions, D)
+        cos.copy_(c2)
+        sin.copy_(s2)
+        qkv.copy_(torch.randn(qkv.shape, generator=gen).bfloat16().to(device))
+        before_k, before_v = k.clone(), v.clone()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        ek, ev, expected = _expected_fused(host_pos, before_k, before_v, q, kn, vn, cos, sin)
+        assert np.array_equal(bits(k), ek) and np.array_equal(bits(v), ev)
+        assert_attention_close(f64(out)[:, 0], expected[:, 0])
+
+
+def test_attention_dropin_signature_and_errors(pkg, device):
+    """npu_attention.attention's contract (npu_attention.py:11-26): BNSD in, BSND out,
+    ValueError for training, dropout and sliding windows."""
+    class Module:
+        training = False
+        sliding_window = None
+
+    k, v = _arena(4, 64, torch.bfloat16, device, 51)
+    gen = torch.Generator().manual_seed(52)
+    q = torch.randn(4, HQ, 1, D, generator=gen).bfloat16().to(device)
+    positions = torch.tensor([3, 10, 63, 0])
+    allowed = torch.arange(64)[None, :] <= positions[:, None]
+    mask = torch.where(allowed, 0.0, torch.finfo(torch.bfloat16).min).bfloat16()[:, None, None, :]
+    out, weights = pkg.attention(Module(), q, k, v, mask.to(device), dropout=0.0, scaling=D ** -0.5,
+                                 sliding_window=None)
+    assert weights is None and out.shape == (4, 1, HQ, D) and out.is_contiguous()
+    expected = oatt.decode_attention(f64(q.transpose(1, 2)), f64(k), f64(v), positions.numpy(), D ** -0.5)
+    assert_attention_close(f64(out), expected)
+    module = Module()
+    module.training = True
+    with pytest.raises(ValueError):
+        pkg.attention(module, q, k, v, None)
+    with pytest.raises(ValueError):
+        pkg.attention(Module(), q, k, v, None, dropout=0.1)
+    module = Module()
+    module.sliding_window = 128
+    with pytest.raises(ValueError):
+        pkg.attention(module, q, k, v, None)
