@@ -101,7 +101,7 @@ def main():
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=200)
     parser.add_argument("--warmup", type=int, default=10)
-    parser.add_argument("--splits", type=int, default=0, help="workgroups per KV head (0 = default)")
+    parser.add_argument("--bins", type=int, default=0, help="workgroups per KV head (0 = one per CU)")
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--calibrate-bytes", type=int, default=0,
@@ -134,9 +134,12 @@ def main():
                       row[..., (HQ + HKV) * D:].view(BATCH, 1, HKV, D),
                       arena[layer], arena[LAYERS + layer], out[layer]))
 
+    plan = pkg.decode_plan(positions, CAPACITY, args.bins)
+
     def step():
+        plan.rebuild()  # one planning launch per step, shared by the 28 layers
         for q, k, v, ak, av, o in views:
-            pkg.decode_step(q, k, v, ak, av, positions, cos, sin, out=o, splits_per_head=args.splits)
+            pkg.decode_step(q, k, v, ak, av, positions, cos, sin, out=o, plan=plan)
 
     step()  # eager: sizes the workspace before capture
     torch.cuda.synchronize()
@@ -165,12 +168,12 @@ def main():
     # attention alone: the non-fused kernel over the already-written arena, same graph method
     q0 = views[0][0].contiguous()
     attn_graph = torch.cuda.CUDAGraph()
-    pkg.decode_attention(q0, arena[0], arena[LAYERS], positions, splits_per_head=args.splits)
+    pkg.decode_attention(q0, arena[0], arena[LAYERS], positions, plan=plan)
     torch.cuda.synchronize()
     with torch.cuda.graph(attn_graph):
         for layer in range(LAYERS):
             pkg.decode_attention(q0, arena[layer], arena[LAYERS + layer], positions,
-                                 out=out[layer], splits_per_head=args.splits)
+                                 out=out[layer], plan=plan)
     attn_graph.replay()
     torch.cuda.synchronize()
     reps = max(1, args.steps // 4)
@@ -218,7 +221,7 @@ def main():
                    "us_per_layer_launch": launch_us,
                    "us_per_layer_attention_only": attn_us,
                    "attention_only_GBs": attention_bytes(contexts) / (attn_us * 1e-6) / 1e9,
-                   "splits_per_head": args.splits or "default",
+                   "bins_per_kv_head": plan.bins,
                    "wall_s_timed_region": wall},
     }
     if not args.no_cpu_baseline:

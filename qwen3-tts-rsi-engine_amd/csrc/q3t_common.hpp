@@ -18,19 +18,27 @@ Q3T_DEVICE float bf16_to_float(uint32_t bits16) { return __uint_as_float(bits16 
 Q3T_DEVICE float bf16_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
 Q3T_DEVICE float bf16_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u); }
 
-// fp32 -> bf16 bits, round-to-nearest-even; NaN maps to 0x7fc0 as c10::BFloat16 does.
-Q3T_DEVICE uint32_t float_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> packed bf16 (lo, hi), round-to-nearest-even, by gfx950's v_cvt_pk_bf16_f32.
+// For every non-NaN input this equals torch's integer rule bf16 = (u + 0x7fff + lsb) >> 16.
+Q3T_DEVICE uint32_t cvt_pk_bf16(float lo, float hi) {
+    const f32x2_t v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
+// Same, with NaN mapped to 0x7fc0 as c10::BFloat16 does.
+Q3T_DEVICE uint32_t cvt_pk_bf16_canon(float lo, float hi) {
+    uint32_t r = cvt_pk_bf16(lo, hi);
+    if (lo != lo) r = (r & 0xffff0000u) | 0x7fc0u;
+    if (hi != hi) r = (r & 0x0000ffffu) | 0x7fc00000u;
+    return r;
+}
+// fp32 -> bf16 bits (canonical NaN), for single values.
+Q3T_DEVICE uint32_t float_to_bf16(float f) { return cvt_pk_bf16_canon(f, 0.f) & 0xffffu; }
 // Round through bf16 and back (one torch-eager bf16 op boundary).
 Q3T_DEVICE float round_bf16(float f) { return bf16_to_float(float_to_bf16(f)); }
 
-Q3T_DEVICE uint32_t pack_bf16(float lo, float hi) {
-    return float_to_bf16(lo) | (float_to_bf16(hi) << 16);
-}
+Q3T_DEVICE uint32_t pack_bf16(float lo, float hi) { return cvt_pk_bf16_canon(lo, hi); }
 
 // a.lo*b.lo + a.hi*b.hi + c on packed bf16 pairs (v_dot2c_f32_bf16).
 Q3T_DEVICE float dot2_bf16(uint32_t a, uint32_t b, float c) {
@@ -55,6 +63,28 @@ Q3T_DEVICE float sum8(float x) {
     return x;
 }
 
+// Value of the lane whose index differs in bit 3 / 4 / 5, without LDS traffic:
+// DPP row_ror:8 inside each 16-lane row, then the gfx950 permlane16/32 swaps.
+Q3T_DEVICE float xor8(float x) { return dpp<0x128>(x); }
+Q3T_DEVICE float xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+}
+Q3T_DEVICE float xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
+// A wave-uniform pointer moved to scalar registers.  readfirstlane is a 32-bit operation, so
+// the two halves of the address go through it separately.
+template <typename P>
+Q3T_DEVICE P *uniform_ptr(P *ptr) {
+    const uint64_t x = reinterpret_cast<uint64_t>(ptr);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)x);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(x >> 32));
+    return reinterpret_cast<P *>(((uint64_t)hi << 32) | lo);
+}
+
 struct alignas(16) U4 { uint32_t x, y, z, w; };
 
 Q3T_DEVICE U4 load16(const void *p) { return *reinterpret_cast<const U4 *>(p); }
@@ -68,21 +98,14 @@ Q3T_DEVICE void store16(void *p, U4 v) { *reinterpret_cast<U4 *>(p) = v; }
 // the same double rounding torch performs for a bf16 add.
 Q3T_DEVICE void rope_pair(uint32_t x1, uint32_t x2, uint32_t c1, uint32_t c2, uint32_t s1,
                           uint32_t s2, uint32_t &y1, uint32_t &y2) {
-    float a[2] = {bf16_lo(x1), bf16_hi(x1)}, b[2] = {bf16_lo(x2), bf16_hi(x2)};
-    float cc1[2] = {bf16_lo(c1), bf16_hi(c1)}, cc2[2] = {bf16_lo(c2), bf16_hi(c2)};
-    float ss1[2] = {bf16_lo(s1), bf16_hi(s1)}, ss2[2] = {bf16_lo(s2), bf16_hi(s2)};
-    uint32_t o1[2], o2[2];
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        float left = round_bf16(a[e] * cc1[e]);
-        float right = round_bf16(-(b[e] * ss1[e]));
-        o1[e] = float_to_bf16(left + right);
-        float left2 = round_bf16(b[e] * cc2[e]);
-        float right2 = round_bf16(a[e] * ss2[e]);
-        o2[e] = float_to_bf16(left2 + right2);
-    }
-    y1 = o1[0] | (o1[1] << 16);
-    y2 = o2[0] | (o2[1] << 16);
+    const float a0 = bf16_lo(x1), a1 = bf16_hi(x1), b0 = bf16_lo(x2), b1 = bf16_hi(x2);
+    // intermediate roundings: a NaN only has to stay a NaN, its bits are canonicalised at the end
+    const uint32_t l1 = cvt_pk_bf16(a0 * bf16_lo(c1), a1 * bf16_hi(c1));
+    const uint32_t r1 = cvt_pk_bf16(-(b0 * bf16_lo(s1)), -(b1 * bf16_hi(s1)));
+    y1 = cvt_pk_bf16_canon(bf16_lo(l1) + bf16_lo(r1), bf16_hi(l1) + bf16_hi(r1));
+    const uint32_t l2 = cvt_pk_bf16(b0 * bf16_lo(c2), b1 * bf16_hi(c2));
+    const uint32_t r2 = cvt_pk_bf16(a0 * bf16_lo(s2), a1 * bf16_hi(s2));
+    y2 = cvt_pk_bf16_canon(bf16_lo(l2) + bf16_lo(r2), bf16_hi(l2) + bf16_hi(r2));
 }
 
 // RoPE on 8 consecutive dims of each half (one 16-byte vector per half).

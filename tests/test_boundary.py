@@ -69,9 +69,13 @@ def test_rejected_calls_return_negative_status_without_a_gpu(pkg):
     args.query = args.keys = args.values = args.positions = args.out = 16
     args.dtype = 0
     assert lib.q3t_decode_attention(args, None) == -2   # head_dim 96 not compiled
-    args.head_dim, args.splits_per_head = 128, 4
+    args.head_dim, args.bins = 128, 4
     assert lib.q3t_decode_attention(args, None) == -3   # no workspace
-    assert lib.q3t_decode_workspace_bytes(64, 1, 16, 8, 128, 64) == 65536 * 4 + 8 * 64 * 2 * 2 * 130 * 4
+    # header 8, per-bin counts (padded to 8), per bin (batch // bins + 2) 8-int records
+    plan_bytes = (8 + 64 + 64 * (64 // 64 + 2) * 8) * 4
+    assert lib.q3t_decode_plan_bytes(64, 64) == plan_bytes
+    assert lib.q3t_decode_workspace_bytes(64, 1, 16, 8, 128, 64) == (
+        65536 * 4 + (plan_bytes + 255) // 256 * 256 + 8 * (64 + 64) * 2 * 130 * 4)
 
 
 def test_wrappers_reject_cpu_tensors(pkg):
