@@ -101,7 +101,8 @@ def main():
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=200)
     parser.add_argument("--warmup", type=int, default=10)
-    parser.add_argument("--bins", type=int, default=0, help="workgroups per KV head (0 = one per CU)")
+    parser.add_argument("--max-chunks", type=int, default=0,
+                        help="64-key chunks (workgroups) per request and KV head (0 = default)")
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--calibrate-bytes", type=int, default=0,
@@ -134,12 +135,9 @@ def main():
                       row[..., (HQ + HKV) * D:].view(BATCH, 1, HKV, D),
                       arena[layer], arena[LAYERS + layer], out[layer]))
 
-    plan = pkg.decode_plan(positions, CAPACITY, args.bins)
-
     def step():
-        plan.rebuild()  # one planning launch per step, shared by the 28 layers
         for q, k, v, ak, av, o in views:
-            pkg.decode_step(q, k, v, ak, av, positions, cos, sin, out=o, plan=plan)
+            pkg.decode_step(q, k, v, ak, av, positions, cos, sin, out=o, max_chunks=args.max_chunks)
 
     step()  # eager: sizes the workspace before capture
     torch.cuda.synchronize()
@@ -168,12 +166,12 @@ def main():
     # attention alone: the non-fused kernel over the already-written arena, same graph method
     q0 = views[0][0].contiguous()
     attn_graph = torch.cuda.CUDAGraph()
-    pkg.decode_attention(q0, arena[0], arena[LAYERS], positions, plan=plan)
+    pkg.decode_attention(q0, arena[0], arena[LAYERS], positions, max_chunks=args.max_chunks)
     torch.cuda.synchronize()
     with torch.cuda.graph(attn_graph):
         for layer in range(LAYERS):
             pkg.decode_attention(q0, arena[layer], arena[LAYERS + layer], positions,
-                                 out=out[layer], plan=plan)
+                                 out=out[layer], max_chunks=args.max_chunks)
     attn_graph.replay()
     torch.cuda.synchronize()
     reps = max(1, args.steps // 4)
@@ -221,7 +219,7 @@ def main():
                    "us_per_layer_launch": launch_us,
                    "us_per_layer_attention_only": attn_us,
                    "attention_only_GBs": attention_bytes(contexts) / (attn_us * 1e-6) / 1e9,
-                   "bins_per_kv_head": plan.bins,
+                   "max_chunks": args.max_chunks,
                    "wall_s_timed_region": wall},
     }
     if not args.no_cpu_baseline:

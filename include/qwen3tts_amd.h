@@ -115,9 +115,10 @@ int q3t_rope_tables(const int64_t *positions, int64_t n, const float *inv_freq, 
  * as SDPA does (bool masks: nonzero attends).  Requests with p_b outside [0, ctx) attend
  * nothing and get zero rows.  Query head hq reads KV head hq / (q_heads / kv_heads).
  *
- * Work follows a plan (q3t_decode_plan) that packs the requests' keys into `bins` bins per
- * KV head; a request longer than a bin's share is split and its partial softmax states are
- * merged across workgroups through `workspace`.  Without a plan the call builds one first.
+ * Keys are cut into chunks of 64 consecutive keys (runs of several such blocks when a
+ * request has more than `max_chunks` blocks); every (request, chunk, KV head) is one
+ * workgroup.  A request with several chunks merges the chunks' partial softmax states
+ * through `workspace`; the last chunk to finish writes the output.
  *
  * fused != 0 additionally performs, for query_len == 1:
  *   - RoPE of the query rows and of the new key with cos/sin rows (bf16-exact, as q3t_rotary),
@@ -155,33 +156,18 @@ typedef struct q3t_decode_args {
     int64_t nk_stride_b, nk_stride_h, nv_stride_b, nv_stride_h;
     const void *cos, *sin;
     int64_t cs_stride_b;
-    /* workspace: a fixed 256 KiB counter region (kv_heads * batch <= 65536), room for a plan,
-       then the partial states of split requests; zero-filled before first use, its counters
-       left zeroed by every launch */
+    /* workspace: a fixed 256 KiB counter region (kv_heads * batch <= 65536), then the
+       partial states of multi-chunk requests; zero-filled before first use, its counters
+       left zeroed by every launch.  Launches that overlap in time must not share one. */
     void *workspace;
     int64_t workspace_bytes;
-    int64_t bins;            /* bins (workgroups) per KV head; <= 0 selects one per CU */
-    const void *plan;        /* optional: q3t_decode_plan output for these positions and bins */
-    int64_t plan_bytes;
+    int64_t max_chunks;      /* chunks per request and KV head, <= 1024; <= 0 selects 64 */
 } q3t_decode_args;
 
 /* Bytes of workspace needed by q3t_decode_attention for these sizes. */
 int64_t q3t_decode_workspace_bytes(int64_t batch, int64_t query_len, int64_t q_heads,
-                                   int64_t kv_heads, int64_t head_dim, int64_t bins);
-
-/* Bytes of a decode plan for `batch` requests over `bins` bins (bins <= 0: default for 8 KV
- * heads). */
-int64_t q3t_decode_plan_bytes(int64_t batch, int64_t bins);
-
-/*
- * Build the work plan of one decode step from the device positions: per-request key counts
- * L_b = p_b + 1 (0 outside [0, ctx)), requests longer than ceil(sum L / bins) cut into
- * near-equal pieces, pieces ranked by length and dealt to bins in snake order.  One small
- * launch; every layer of the step can reuse the plan while positions stay unchanged.
- * Replaces: the per-step preparation SlotCache.prepare (continuous.py:147-150, 189).
- */
-int q3t_decode_plan(const int64_t *positions, int64_t batch, int64_t ctx, int64_t bins,
-                    void *plan, int64_t plan_bytes, void *stream);
+                                   int64_t kv_heads, int64_t head_dim, int64_t ctx,
+                                   int64_t max_chunks);
 
 int q3t_decode_attention(const q3t_decode_args *args, void *stream);
 

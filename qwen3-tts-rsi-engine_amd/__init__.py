@@ -20,13 +20,12 @@ from .batching import decode_batch_size
 from .packed_kv import copy_packed_prefix, copy_rows
 from .kv_write import write, write_tokens
 from .rotary import rotary, rope_tables, inverse_frequencies
-from .attention import (DecodePlan, attention, decode_attention, decode_plan, decode_step,
-                        prefill_attention)
+from .attention import attention, decode_attention, decode_step, prefill_attention
 
 __all__ = [
     "decode_batch_size", "copy_packed_prefix", "copy_rows", "write", "write_tokens", "rotary",
     "rope_tables", "inverse_frequencies", "attention", "decode_attention", "decode_step",
-    "prefill_attention", "decode_plan", "DecodePlan", "library",
+    "prefill_attention", "library",
 ]
 
 library = _lib.library

@@ -45,8 +45,7 @@ class DecodeArgs(ctypes.Structure):
         ("new_key", c_vp), ("new_value", c_vp),
         ("nk_stride_b", c_i64), ("nk_stride_h", c_i64), ("nv_stride_b", c_i64), ("nv_stride_h", c_i64),
         ("cos", c_vp), ("sin", c_vp), ("cs_stride_b", c_i64),
-        ("workspace", c_vp), ("workspace_bytes", c_i64), ("bins", c_i64),
-        ("plan", c_vp), ("plan_bytes", c_i64),
+        ("workspace", c_vp), ("workspace_bytes", c_i64), ("max_chunks", c_i64),
     ]
 
 
@@ -91,9 +90,7 @@ SIGNATURES = {
     "q3t_rotary": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp]),
     "q3t_rope_tables": (ctypes.c_int, [c_vp, c_i64, c_vp, c_i64, ctypes.c_float, c_i64, c_vp,
                                        c_vp, c_vp]),
-    "q3t_decode_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i64]),
-    "q3t_decode_plan_bytes": (c_i64, [c_i64, c_i64]),
-    "q3t_decode_plan": (ctypes.c_int, [c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp]),
+    "q3t_decode_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64]),
     "q3t_decode_attention": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
     "q3t_prefill_attention": (ctypes.c_int, [ctypes.POINTER(PrefillArgs), c_vp]),
     "q3t_prefill_rope_write": (ctypes.c_int, [ctypes.POINTER(PrefillRopeWriteArgs), c_vp]),

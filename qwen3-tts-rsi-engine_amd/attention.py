@@ -53,64 +53,12 @@ def _mask_view(mask, batch, query_len, ctx):
     return mask.expand(batch, query_len, ctx)
 
 
-class DecodePlan:
-    """Work plan of one decode step (q3t_decode_plan): which keys each workgroup streams.
-
-    Built once from the device positions and reused by every layer of the step, as the
-    reference's SlotCache.prepare runs once per step (continuous.py:147-150, 189).  It stays
-    valid while the positions tensor's contents stay unchanged."""
-
-    def __init__(self, positions, ctx, bins=0):
-        if positions.ndim != 1 or positions.dtype != torch.int64:
-            raise ValueError('positions must be an int64 (batch,) tensor')
-        device = _lib.require_gpu(positions)
-        lib = _lib.library()
-        self.batch, self.ctx = positions.shape[0], int(ctx)
-        with torch.cuda.device(device):
-            self.bins = int(bins) if bins and bins > 0 else _default_bins()
-            nbytes = lib.q3t_decode_plan_bytes(self.batch, self.bins)
-        if nbytes < 0 or self.batch < 1:
-            raise ValueError('invalid plan sizes')
-        self.positions = positions
-        self.buffer = torch.empty(nbytes // 4, dtype=torch.int32, device=device)
-        self.rebuild()
-
-    def rebuild(self):
-        """Recompute the plan from the current positions (a single small launch)."""
-        status = _lib.library().q3t_decode_plan(self.positions.data_ptr(), self.batch, self.ctx,
-                                                self.bins, self.buffer.data_ptr(),
-                                                self.buffer.numel() * 4,
-                                                _lib.stream_handle(self.positions.device))
-        _lib.check(status, 'decode plan')
-
-
-def _default_bins(kv_heads=8):
-    """One workgroup per CU: CUs / kv_heads bins per head."""
-    props = torch.cuda.get_device_properties(torch.cuda.current_device())
-    return max(1, min(1024, props.multi_processor_count // kv_heads))
-
-
-def decode_plan(positions, ctx, bins=0):
-    """Plan one decode step for these positions (see DecodePlan)."""
-    return DecodePlan(positions, ctx, bins)
-
-
-def _attach_plan(a, plan, batch, ctx, bins, kv_heads):
-    if plan is not None:
-        if plan.batch != batch or plan.ctx != ctx:
-            raise ValueError('the plan was built for another batch or context')
-        a.bins = plan.bins
-        a.plan = plan.buffer.data_ptr()
-        a.plan_bytes = plan.buffer.numel() * 4
-    else:
-        a.bins = int(bins) if bins and bins > 0 else _default_bins(kv_heads)
-
-
 def _run_decode(args: _lib.DecodeArgs, device: torch.device, what: str) -> None:
     lib = _lib.library()
     with torch.cuda.device(device):
         need = lib.q3t_decode_workspace_bytes(args.batch, args.query_len, args.q_heads,
-                                              args.kv_heads, args.head_dim, args.bins)
+                                              args.kv_heads, args.head_dim, args.ctx,
+                                              args.max_chunks)
         if need < 0:
             raise ValueError(f'{what}: invalid sizes')
         ws = workspace(device, need)
@@ -121,11 +69,12 @@ def _run_decode(args: _lib.DecodeArgs, device: torch.device, what: str) -> None:
 
 
 def decode_attention(query, keys, values, positions, *, scale=None, mask=None, kv_offsets=None,
-                     out=None, plan=None, bins=0):
+                     out=None, max_chunks=0):
     """query (B, S, Hq, D) BSND; keys/values (B, Hkv, ctx, D) views of the arena (or, with
     ``kv_offsets``, any base tensor whose request rows start at those element offsets);
-    positions (B,) int64: the last query position of each request.  ``plan`` (DecodePlan of
-    these positions and ctx) skips the per-call planning launch.  Returns (B, S, Hq, D)."""
+    positions (B,) int64: the last query position of each request.  ``max_chunks`` bounds the
+    64-key chunks (workgroups) per request and KV head (0: the default, 64).
+    Returns (B, S, Hq, D)."""
     if query.ndim != 4 or keys.ndim != 4 or values.shape != keys.shape:
         raise ValueError('expected BSND query and BNSD key/value views')
     batch, qlen, q_heads, head_dim = query.shape
@@ -169,14 +118,13 @@ def decode_attention(query, keys, values, positions, *, scale=None, mask=None, k
         a.mask_stride_b, a.mask_stride_s, a.mask_stride_t = m.stride()
     a.out = out.data_ptr()
     a.o_stride_b, a.o_stride_s, a.o_stride_h = out.stride()[:3]
-    with torch.cuda.device(device):
-        _attach_plan(a, plan, batch, ctx, bins, kv_heads)
+    a.max_chunks = int(max_chunks)
     _run_decode(a, device, 'decode attention')
     return out
 
 
 def decode_step(query, new_key, new_value, key_arena, value_arena, positions, cos, sin, *,
-                scale=None, out=None, plan=None, bins=0):
+                scale=None, out=None, max_chunks=0):
     """Fused one-token decode for a layer.
 
     query (B, 1, Hq, D), new_key/new_value (B, 1, Hkv, D): un-rotated bf16 rows (views of the
@@ -228,8 +176,7 @@ def decode_step(query, new_key, new_value, key_arena, value_arena, positions, co
     a.nv_stride_b, a.nv_stride_h = new_value.stride(0), new_value.stride(2)
     a.cos, a.sin = cos2.data_ptr(), sin2.data_ptr()
     a.cs_stride_b = cos2.stride(0)
-    with torch.cuda.device(device):
-        _attach_plan(a, plan, batch, a.ctx, bins, kv_heads)
+    a.max_chunks = int(max_chunks)
     _run_decode(a, device, 'fused decode step')
     return out
 

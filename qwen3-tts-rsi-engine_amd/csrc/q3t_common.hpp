@@ -11,6 +11,8 @@
 
 namespace q3t {
 
+struct alignas(16) U4 { uint32_t x, y, z, w; };
+
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 // bf16 (as raw 16 bits) -> fp32: exact.
@@ -75,6 +77,15 @@ Q3T_DEVICE float xor32(float x) {
     return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
 }
 
+Q3T_DEVICE uint32_t xor8u(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x128, 0xf, 0xf, false);
+}
+// The 16-byte vector of the lane whose index differs in bit 3 (the other half of a 256-byte
+// row spread over 16 lanes).
+Q3T_DEVICE U4 xor8_u4(const U4 &v) {
+    return U4{xor8u(v.x), xor8u(v.y), xor8u(v.z), xor8u(v.w)};
+}
+
 // A wave-uniform pointer moved to scalar registers.  readfirstlane is a 32-bit operation, so
 // the two halves of the address go through it separately.
 template <typename P>
@@ -85,7 +96,19 @@ Q3T_DEVICE P *uniform_ptr(P *ptr) {
     return reinterpret_cast<P *>(((uint64_t)hi << 32) | lo);
 }
 
-struct alignas(16) U4 { uint32_t x, y, z, w; };
+// Buffer access through a wave-uniform resource: 32-bit byte offsets from the base, reads at
+// or past `bytes` return zeros (the resource's range check).  0x00020000 is the gfx9-family
+// descriptor word 3 for raw 32-bit dword data.
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+Q3T_DEVICE __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+Q3T_DEVICE U4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(U4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+Q3T_DEVICE void buffer_store16(__amdgpu_buffer_rsrc_t r, uint32_t off, U4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, v), r, (int)off, 0, 0);
+}
 
 Q3T_DEVICE U4 load16(const void *p) { return *reinterpret_cast<const U4 *>(p); }
 Q3T_DEVICE void store16(void *p, U4 v) { *reinterpret_cast<U4 *>(p) = v; }
@@ -113,6 +136,25 @@ Q3T_DEVICE void rope8(const uint32_t *x1, const uint32_t *x2, const uint32_t *c1
                       const uint32_t *s1, const uint32_t *s2, uint32_t *y1, uint32_t *y2) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) rope_pair(x1[i], x2[i], c1[i], c2[i], s1[i], s2[i], y1[i], y2[i]);
+}
+
+// RoPE of one 16-byte vector (8 dims) of a row, as rope_pair computes it: `own` holds the
+// lane's dims of one half, `partner` the same dims of the other half, c/s the cos/sin values
+// at own's dims.  First half: bf16(bf16(own*c) + bf16(-(partner*s))); second half:
+// bf16(bf16(own*c) + bf16(partner*s)).
+Q3T_DEVICE U4 rope_half8(U4 own, U4 partner, U4 c, U4 s, bool first) {
+    const uint32_t o[4] = {own.x, own.y, own.z, own.w}, q[4] = {partner.x, partner.y, partner.z, partner.w};
+    const uint32_t cc[4] = {c.x, c.y, c.z, c.w}, ss[4] = {s.x, s.y, s.z, s.w};
+    const uint32_t sign = first ? 0x80000000u : 0u;
+    uint32_t y[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t a = cvt_pk_bf16(bf16_lo(o[i]) * bf16_lo(cc[i]), bf16_hi(o[i]) * bf16_hi(cc[i]));
+        const uint32_t b = cvt_pk_bf16(__uint_as_float(__float_as_uint(bf16_lo(q[i]) * bf16_lo(ss[i])) ^ sign),
+                                       __uint_as_float(__float_as_uint(bf16_hi(q[i]) * bf16_hi(ss[i])) ^ sign));
+        y[i] = cvt_pk_bf16_canon(bf16_lo(a) + bf16_lo(b), bf16_hi(a) + bf16_hi(b));
+    }
+    return U4{y[0], y[1], y[2], y[3]};
 }
 
 inline bool aligned(const void *p, int64_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }

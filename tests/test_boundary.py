@@ -69,13 +69,15 @@ def test_rejected_calls_return_negative_status_without_a_gpu(pkg):
     args.query = args.keys = args.values = args.positions = args.out = 16
     args.dtype = 0
     assert lib.q3t_decode_attention(args, None) == -2   # head_dim 96 not compiled
-    args.head_dim, args.bins = 128, 4
+    args.head_dim = 128
     assert lib.q3t_decode_attention(args, None) == -3   # no workspace
-    # header 8, per-bin counts (padded to 8), per bin (batch // bins + 2) 8-int records
-    plan_bytes = (8 + 64 + 64 * (64 // 64 + 2) * 8) * 4
-    assert lib.q3t_decode_plan_bytes(64, 64) == plan_bytes
-    assert lib.q3t_decode_workspace_bytes(64, 1, 16, 8, 128, 64) == (
-        65536 * 4 + (plan_bytes + 255) // 256 * 256 + 8 * (64 + 64) * 2 * 130 * 4)
+    args.max_chunks = 1025
+    assert lib.q3t_decode_attention(args, None) == -1   # more chunks than supported
+    # 256 KiB of counters, then one (G * query_len) x (head_dim + 2) fp32 state per chunk:
+    # ctx 1024 is 16 chunks of 64 keys, capped by max_chunks (default 64)
+    assert lib.q3t_decode_workspace_bytes(64, 1, 16, 8, 128, 1024, 0) == 65536 * 4 + 64 * 8 * 16 * 2 * 130 * 4
+    assert lib.q3t_decode_workspace_bytes(64, 2, 16, 8, 128, 1024, 4) == 65536 * 4 + 64 * 8 * 4 * 4 * 130 * 4
+    assert lib.q3t_decode_workspace_bytes(64, 1, 16, 8, 128, 1024, 1025) == -1
 
 
 def test_wrappers_reject_cpu_tensors(pkg):

@@ -84,15 +84,15 @@ def _expected_fused(contexts, k, v, q, kn, vn, cos, sin):
     return ak, av, out
 
 
-@pytest.mark.parametrize("bins", [0, 1, 7, 64, 1000])
-def test_config2_fused_decode_step(pkg, device, bins):
+@pytest.mark.parametrize("max_chunks", [0, 1, 3, 16, 1000])
+def test_config2_fused_decode_step(pkg, device, max_chunks):
     """The headline step: RoPE + write + ragged GQA over 64 requests, seed 0 (sum c = 32718)."""
     contexts, k, v, q, kn, vn = _config2(device)
     assert int(contexts.sum()) == 32718
     positions = contexts.to(device)
     cos, sin = pkg.rope_tables(positions, D)
     expected_k, expected_v, expected = _expected_fused(contexts, k, v, q, kn, vn, cos, sin)
-    out = pkg.decode_step(q, kn, vn, k, v, positions, cos, sin, bins=bins)
+    out = pkg.decode_step(q, kn, vn, k, v, positions, cos, sin, max_chunks=max_chunks)
     assert np.array_equal(bits(k), expected_k) and np.array_equal(bits(v), expected_v)
     assert_attention_close(f64(out)[:, 0], expected[:, 0])
 
@@ -284,19 +284,19 @@ def test_attention_dropin_signature_and_errors(pkg, device):
         pkg.attention(module, q, k, v, None)
 
 
-@pytest.mark.parametrize("kv_heads,bins", [(8, 64), (4, 96), (8, 500)])
-def test_split_merge_is_deterministic_across_launches(pkg, device, kv_heads, bins):
-    """Partial states cross workgroups (and, with 4 KV heads, XCDs) through the workspace;
-    the merge runs in a fixed piece order, so repeated launches are bit-identical and match
+@pytest.mark.parametrize("kv_heads,max_chunks", [(8, 0), (4, 5), (8, 2)])
+def test_split_merge_is_deterministic_across_launches(pkg, device, kv_heads, max_chunks):
+    """Chunk states cross workgroups (and, with 4 KV heads, XCDs) through the workspace;
+    the merge runs in a fixed chunk order, so repeated launches are bit-identical and match
     the oracle."""
     gen = torch.Generator().manual_seed(60 + kv_heads)
     contexts = torch.randint(64, 1025, (64,), generator=gen)
     k, v = _arena(64, 1024, torch.bfloat16, device, 61, kv_heads=kv_heads)
     q = torch.randn(64, 1, kv_heads * 2, D, generator=gen).bfloat16().to(device)
     positions = contexts.to(device)
-    first = pkg.decode_attention(q, k, v, positions, bins=bins).clone()
+    first = pkg.decode_attention(q, k, v, positions, max_chunks=max_chunks).clone()
     for _ in range(20):
-        again = pkg.decode_attention(q, k, v, positions, bins=bins)
+        again = pkg.decode_attention(q, k, v, positions, max_chunks=max_chunks)
         assert torch.equal(again, first)
     expected = oatt.decode_attention(f64(q), f64(k), f64(v), contexts.numpy(), D ** -0.5)
     assert_attention_close(f64(first), expected)
