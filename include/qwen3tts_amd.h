@@ -117,7 +117,7 @@ int q3t_rope_tables(const int64_t *positions, int64_t n, const float *inv_freq, 
  *
  * Keys are cut into chunks of 64 consecutive keys (runs of several such blocks when a
  * request has more than `max_chunks` blocks); every (request, chunk, KV head) is one
- * workgroup.  A request with several chunks merges the chunks' partial softmax states
+ * workgroup; chunks past a request's length exit at once.  A request with several chunks merges the chunks' partial softmax states
  * through `workspace`; the last chunk to finish writes the output.
  *
  * fused != 0 additionally performs, for query_len == 1:
@@ -161,7 +161,8 @@ typedef struct q3t_decode_args {
        left zeroed by every launch.  Launches that overlap in time must not share one. */
     void *workspace;
     int64_t workspace_bytes;
-    int64_t max_chunks;      /* chunks per request and KV head, <= 1024; <= 0 selects 64 */
+    int64_t max_chunks;      /* chunks per request and KV head, <= 1024; <= 0: enough for
+                                about 2048 workgroups over the batch */
 } q3t_decode_args;
 
 /* Bytes of workspace needed by q3t_decode_attention for these sizes. */

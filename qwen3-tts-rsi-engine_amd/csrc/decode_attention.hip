@@ -33,7 +33,6 @@ namespace q3t {
 constexpr int kMaxBatch = 1024;
 constexpr int kChunkRows = 64;
 constexpr int kMaxChunks = 1024;
-constexpr int kDefaultMaxChunks = 64;
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -362,21 +361,32 @@ decode_attention_kernel(DecodeParams p) {
         }
     };
 
+    // keys of the block at jb: rows at or past jend get an offset outside the resource, which
+    // reads zeros without a memory access
+    auto load_block = [&](int jb, U4 (&kr)[P], U4 (&vr)[P]) {
+#pragma unroll
+        for (int pp = 0; pp < P; ++pp) {
+            const int j = jb + pp * RPP + wave * RPW + grp;
+            const bool ok = j < jend;
+            const uint32_t ko = ok ? (uint32_t)(j * kst) + cl * 16 : 0xfffffff0u;
+            const uint32_t vo = ok ? (same_stride ? ko : (uint32_t)(j * vst) + cl * 16) : 0xfffffff0u;
+            kr[pp] = buffer_load16(krs, ko);
+            vr[pp] = buffer_load16(vrs, vo);
+        }
+    };
+    auto block_keys = [&](int jb, int (&kidx)[P], bool (&valid)[P]) {
+#pragma unroll
+        for (int pp = 0; pp < P; ++pp) {
+            kidx[pp] = jb + pp * RPP + wave * RPW + grp;
+            valid[pp] = kidx[pp] < jend;
+        }
+    };
     for (int jb = j0; jb < jend; jb += kChunkRows) {
         U4 kr[P], vr[P];
         int kidx[P];
         bool valid[P];
-#pragma unroll
-        for (int pp = 0; pp < P; ++pp) {
-            const int j = jb + pp * RPP + wave * RPW + grp;
-            kidx[pp] = j;
-            valid[pp] = j < jend;
-            const int js = valid[pp] ? j : jb;
-            const uint32_t ko = (uint32_t)(js * kst) + cl * 16;
-            const uint32_t vo = same_stride ? ko : (uint32_t)(js * vst) + cl * 16;
-            kr[pp] = buffer_load16(krs, ko);
-            vr[pp] = buffer_load16(vrs, vo);
-        }
+        load_block(jb, kr, vr);
+        block_keys(jb, kidx, valid);
         step(kr, vr, kidx, valid, jb != j0);
     }
     if constexpr (FUSED) {
@@ -493,9 +503,17 @@ decode_attention_kernel(DecodeParams p) {
 constexpr int64_t kMaxCounters = 65536;  // batch * kv_heads
 static int64_t counters_bytes() { return kMaxCounters * 4; }
 
-static int64_t chunk_count(int64_t ctx, int64_t max_chunks) {
-    if (max_chunks <= 0) max_chunks = kDefaultMaxChunks;
+// Chunks per (request, KV head): ceil(ctx / 64) at most; by default as many as keep about
+// kTargetGroups workgroups in flight for the whole batch (fewer chunks mean fewer partial
+// states to merge, more mean more parallelism for small batches).
+constexpr int64_t kTargetGroups = 2048;
+static int64_t chunk_count(int64_t batch, int64_t kv_heads, int64_t ctx, int64_t max_chunks) {
     const int64_t blocks = (ctx + kChunkRows - 1) / kChunkRows;
+    if (max_chunks <= 0) {
+        const int64_t units = batch * kv_heads > 0 ? batch * kv_heads : 1;
+        max_chunks = (kTargetGroups + units - 1) / units;
+        if (max_chunks > kMaxChunks) max_chunks = kMaxChunks;
+    }
     return blocks < max_chunks ? blocks : max_chunks;
 }
 
@@ -510,7 +528,7 @@ extern "C" int64_t q3t_decode_workspace_bytes(int64_t batch, int64_t query_len, 
         head_dim < 1 || ctx < 1 || ctx > (1 << 20) || max_chunks > kMaxChunks)
         return -1;
     const int64_t R = (q_heads / kv_heads) * query_len;
-    return counters_bytes() + batch * kv_heads * chunk_count(ctx, max_chunks) * R * (head_dim + 2) * 4;
+    return counters_bytes() + batch * kv_heads * chunk_count(batch, kv_heads, ctx, max_chunks) * R * (head_dim + 2) * 4;
 }
 
 template <typename T, int D, int G, int SQ, bool F, bool M>
@@ -586,7 +604,7 @@ extern "C" int q3t_decode_attention(const q3t_decode_args *a, void *stream) {
     // key rows are addressed by 32-bit byte offsets from a request's base
     const int64_t max_st = a->k_stride_t > a->v_stride_t ? a->k_stride_t : a->v_stride_t;
     if (max_st < 0 || a->ctx * max_st * es + a->head_dim * es > INT32_MAX) return Q3T_EUNSUPPORTED;
-    const int64_t nchunks = chunk_count(a->ctx, a->max_chunks);
+    const int64_t nchunks = chunk_count(a->batch, a->kv_heads, a->ctx, a->max_chunks);
     if (a->batch * a->kv_heads * nchunks > INT32_MAX) return Q3T_EUNSUPPORTED;
     const int64_t need = q3t_decode_workspace_bytes(a->batch, a->query_len, a->q_heads, a->kv_heads,
                                                     a->head_dim, a->ctx, a->max_chunks);
