@@ -11,14 +11,21 @@ import numpy as np
 
 
 def decode_batch_size(active, max_slots, step=0):
-    """batching.py:4-11."""
-    if not 1 <= active <= max_slots or max_slots & (max_slots - 1):
+    """batching.py:4-11, restated as a search: the smallest admissible bucket that holds
+    ``active`` requests.  Admissible buckets are the powers of two up to the step (all of
+    them without a step) and then the multiples of the step; both rules require a
+    power-of-two arena and a power-of-two step no larger than it."""
+    def pow2(n):
+        return n > 0 and (n & (n - 1)) == 0
+    if not pow2(max_slots) or active < 1 or active > max_slots:
         raise ValueError('Active count must fit a positive power-of-two slot arena')
-    if step < 0 or (step and (step & (step - 1) or step > max_slots)):
+    if step < 0 or (step > 0 and (not pow2(step) or step > max_slots)):
         raise ValueError('Decode bucket step must be zero or a power of two within the arena')
-    if not step or active <= step:
-        return 1 << (active - 1).bit_length()
-    return ((active + step - 1) // step) * step
+    limit = step if step else max_slots
+    candidates = [1 << e for e in range(max_slots.bit_length()) if (1 << e) <= limit]
+    if step:
+        candidates += list(range(2 * step, max_slots + 1, step))
+    return min(c for c in candidates if c >= active)
 
 
 @dataclass
