@@ -177,7 +177,9 @@ int q3t_decode_attention(const q3t_decode_args *args, void *stream);
  * Requests are packed along the token axis by cu_seqlens (batch + 1, int32, device):
  * query rows (tokens, q_heads, head_dim); key/value rows are read from the slot arena
  * (slot = kv_slots ? kv_slots[b] : b) at positions 0 ... len_b - 1, with strides as in
- * q3t_decode_args.  Query token i of request b attends keys 0 ... i.
+ * q3t_decode_args.  Query token i of request b attends keys 0 ... i (keys at or past
+ * `capacity` do not exist).  max_seqlen bounds len_b; query blocks past it are not computed.
+ * bf16 only; head_dim 64 or 128; q_heads / kv_heads in {1, 2, 4}.
  * Replaces: PrefillGraph.compute's padded causal attention (prefill_graph.py:31-50) for
  * the valid rows of each request.
  */
@@ -193,6 +195,7 @@ typedef struct q3t_prefill_args {
     const int64_t *kv_slots;       /* optional device (batch,) */
     void *out;                     /* (tokens, q_heads, head_dim) bf16 */
     int64_t o_stride_t, o_stride_h;
+    int64_t capacity;              /* key rows per slot in the arena views */
 } q3t_prefill_args;
 
 int q3t_prefill_attention(const q3t_prefill_args *args, void *stream);

@@ -21,11 +21,12 @@ from .packed_kv import copy_packed_prefix, copy_rows
 from .kv_write import write, write_tokens
 from .rotary import rotary, rope_tables, inverse_frequencies
 from .attention import attention, decode_attention, decode_step, prefill_attention
+from .prefill import prefill_rope_write, prefill_step
 
 __all__ = [
     "decode_batch_size", "copy_packed_prefix", "copy_rows", "write", "write_tokens", "rotary",
     "rope_tables", "inverse_frequencies", "attention", "decode_attention", "decode_step",
-    "prefill_attention", "library",
+    "prefill_attention", "prefill_rope_write", "prefill_step", "library",
 ]
 
 library = _lib.library

@@ -59,6 +59,7 @@ class PrefillArgs(ctypes.Structure):
         ("k_stride_b", c_i64), ("k_stride_h", c_i64), ("k_stride_t", c_i64),
         ("v_stride_b", c_i64), ("v_stride_h", c_i64), ("v_stride_t", c_i64),
         ("kv_slots", c_vp), ("out", c_vp), ("o_stride_t", c_i64), ("o_stride_h", c_i64),
+        ("capacity", c_i64),
     ]
 
 

@@ -256,6 +256,7 @@ def prefill_attention(query, keys, values, cu_seqlens, max_seqlen, *, scale=None
         a.kv_slots = kv_slots.data_ptr()
     a.out = out.data_ptr()
     a.o_stride_t, a.o_stride_h = out.stride()[:2]
+    a.capacity = keys.shape[2]
     status = _lib.library().q3t_prefill_attention(a, _lib.stream_handle(device))
     _lib.check(status, 'prefill attention')
     return out

@@ -60,8 +60,6 @@ struct DecodeParams {
     int *counters;
 };
 
-Q3T_DEVICE float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
 Q3T_DEVICE int mask_elem_size(int dtype) { return dtype == Q3T_F32 ? 4 : dtype == Q3T_BOOL ? 1 : 2; }
 
 Q3T_DEVICE float load_mask(const char *m, int dtype) {

@@ -76,6 +76,213 @@ __global__ void __launch_bounds__(256) prefill_rope_write_kernel(PrefillRopeWrit
     }
 }
 
+
+// ---- varlen causal attention on bf16 MFMA tiles ------------------------------------------
+//
+// One workgroup of 4 waves per (request, 64-query block, KV head); wave w owns queries
+// q0 + 16w ... q0 + 16w + 15 of all G query heads that share the KV head.  Keys stream in
+// tiles of 32 through LDS: K row-major, V transposed, so that both products read 16-byte
+// (K) or 8-byte (V) runs.  With v_mfma_f32_16x16x32_bf16 (lane l = 16g + c holds
+// A[c][8g..8g+7], B[8g..8g+7][c] and D[4g..4g+3][c]):
+//   S^T (keys x queries) = K . Q^T   A = K rows from LDS, B = the wave's Q rows (registers);
+//                                    lane (g, c) gets keys 4g..4g+3 of query c per 16 keys;
+//   O^T (dims x queries) += V^T . P^T   B = P^T straight from the S^T registers, its K index
+//                                    ordering keys {4g..4g+3, 16+4g..16+4g+3}; A = V^T rows
+//                                    read from LDS in that same key order.
+// Each lane therefore keeps the online-softmax state of one query per head, with no data
+// movement between the two products.
+constexpr int kQBlock = 64;
+constexpr int kKTile = 32;
+constexpr float kLog2eP = 1.4426950408889634f;
+constexpr float kEmptyP = -1.0e30f;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+struct PrefillParams {
+    int B, Hq, Hkv, nqb;
+    int64_t T;
+    float scale_log2;
+    const int32_t *cu;
+    const char *q;
+    int64_t q_st, q_sh;
+    const char *k, *v;
+    int64_t k_sb, k_sh, k_st, v_sb, v_sh, v_st;
+    int64_t cap;
+    const int64_t *slots;
+    char *out;
+    int64_t o_st, o_sh;
+};
+
+Q3T_DEVICE bf16x8_t as_bf16x8(const U4 &v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+template <int D, int G>
+__global__ void __launch_bounds__(256) prefill_attention_kernel(PrefillParams p) {
+    constexpr int KK = D / 32;   // MFMA steps over the head dimension
+    constexpr int DB = D / 16;   // 16-row blocks of O^T
+    constexpr int KROW = D + 8;  // padded LDS row of K (bf16)
+    constexpr int VROW = kKTile + 4;
+    constexpr int CPR = D / 8;   // 16-byte chunks per row
+    __shared__ uint16_t sK[kKTile][KROW];
+    __shared__ uint16_t sVt[D][VROW];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int h = blockIdx.x % p.Hkv;
+    const int rest = blockIdx.x / p.Hkv;
+    const int b = rest % p.B;
+    const int qb = p.nqb - 1 - rest / p.B;  // the longest blocks are dispatched first
+    const int t0 = p.cu[b];
+    if (t0 < 0 || t0 >= p.T) return;
+    const int n = (int)min((int64_t)(p.cu[b + 1] - t0), p.T - t0);  // rows past the packed tokens do not exist
+    const int q0 = qb * kQBlock;
+    if (q0 >= n) return;
+    // keys 0 ... kv_end-1 are visible to this block; the arena holds at most `cap` of them
+    const int kv_end = (int)min((int64_t)min(n, q0 + kQBlock), p.cap);
+    const int ntiles = (kv_end + kKTile - 1) / kKTile;
+    const int64_t slot = p.slots ? p.slots[b] : b;
+
+    // the wave's query rows as B operands: Q[query c][8g + 32kk ...], zeros past the request
+    const int qpos = q0 + 16 * wave + c;
+    const bool qvalid = qpos < n;
+    bf16x8_t qB[G][KK];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        const char *row = p.q + ((int64_t)(t0 + (qvalid ? qpos : 0)) * p.q_st + (h * G + j) * p.q_sh) * 2;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            U4 v = load16(row + (32 * kk + 8 * g) * 2);
+            if (!qvalid) v = U4{0u, 0u, 0u, 0u};
+            qB[j][kk] = as_bf16x8(v);
+        }
+    }
+
+    // K/V tile loader: 256 threads x 16 bytes per pass; rows past kv_end read zeros
+    const char *kbase = p.k + (slot * p.k_sb + h * p.k_sh) * 2;
+    const char *vbase = p.v + (slot * p.v_sb + h * p.v_sh) * 2;
+    const auto krs = buffer_rsrc(uniform_ptr(kbase), (uint32_t)((kv_end - 1) * p.k_st * 2 + D * 2));
+    const auto vrs = buffer_rsrc(uniform_ptr(vbase), (uint32_t)((kv_end - 1) * p.v_st * 2 + D * 2));
+    constexpr int PASSES = kKTile * CPR / 256;
+    U4 kreg[PASSES], vreg[PASSES];
+    auto fetch = [&](int kt) {
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps) {
+            const int idx = ps * 256 + tid, row = idx / CPR, ch = idx % CPR;
+            const int key = kt * kKTile + row;
+            const bool ok = key < kv_end;
+            kreg[ps] = buffer_load16(krs, ok ? (uint32_t)(key * p.k_st * 2 + ch * 16) : 0xfffffff0u);
+            vreg[ps] = buffer_load16(vrs, ok ? (uint32_t)(key * p.v_st * 2 + ch * 16) : 0xfffffff0u);
+        }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps) {
+            const int idx = ps * 256 + tid, row = idx / CPR, ch = idx % CPR;
+            *reinterpret_cast<U4 *>(&sK[row][ch * 8]) = kreg[ps];
+            const uint32_t w[4] = {vreg[ps].x, vreg[ps].y, vreg[ps].z, vreg[ps].w};
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                sVt[ch * 8 + 2 * m][row] = (uint16_t)(w[m] & 0xffffu);
+                sVt[ch * 8 + 2 * m + 1][row] = (uint16_t)(w[m] >> 16);
+            }
+        }
+    };
+
+    f32x4_t acc[G][DB];
+    float m[G], l[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        m[j] = kEmptyP;
+        l[j] = 0.f;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) acc[j][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+
+    fetch(0);
+    for (int kt = 0; kt < ntiles; ++kt) {
+        __syncthreads();  // every wave is done reading the previous tile
+        stage();
+        __syncthreads();
+        if (kt + 1 < ntiles) fetch(kt + 1);  // in flight during this tile's products
+        const int kbase_idx = kt * kKTile;
+        if (kbase_idx > q0 + 16 * wave + 15) continue;  // the whole tile is above this wave's diagonal
+
+        // S^T for both 16-key halves of the tile and every head
+        f32x4_t st[2][G];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int j = 0; j < G; ++j) st[kb][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+                const bf16x8_t a = as_bf16x8(*reinterpret_cast<const U4 *>(&sK[16 * kb + c][32 * kk + 8 * g]));
+#pragma unroll
+                for (int j = 0; j < G; ++j)
+                    st[kb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qB[j][kk], st[kb][j], 0, 0, 0);
+            }
+        }
+        // scale, causal mask, online softmax per (head, query c); P^T packed to bf16
+        bf16x8_t pB[G];
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            float x[8];
+            float mx = kEmptyP;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int key = kbase_idx + 16 * kb + 4 * g + i;
+                    const float s = st[kb][j][i] * p.scale_log2;
+                    x[kb * 4 + i] = (key <= qpos && key < kv_end) ? s : -INFINITY;
+                    mx = fmaxf(mx, x[kb * 4 + i]);
+                }
+            mx = fmaxf(mx, xor16(mx));
+            mx = fmaxf(mx, xor32(mx));
+            const float mn = fmaxf(m[j], mx);
+            const float alpha = fexp2(m[j] - mn);
+            m[j] = mn;
+            float ps = 0.f;
+            float pv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                pv[e] = fexp2(x[e] - mn);
+                ps += pv[e];
+            }
+            l[j] = l[j] * alpha + ps;  // this lane's keys only; summed over g at the end
+#pragma unroll
+            for (int db = 0; db < DB; ++db) acc[j][db] *= alpha;
+            const U4 packed = {cvt_pk_bf16(pv[0], pv[1]), cvt_pk_bf16(pv[2], pv[3]),
+                               cvt_pk_bf16(pv[4], pv[5]), cvt_pk_bf16(pv[6], pv[7])};
+            pB[j] = as_bf16x8(packed);
+        }
+        // O^T += V^T . P^T
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            const uint2 lo = *reinterpret_cast<const uint2 *>(&sVt[16 * db + c][4 * g]);
+            const uint2 hi = *reinterpret_cast<const uint2 *>(&sVt[16 * db + c][16 + 4 * g]);
+            const bf16x8_t a = as_bf16x8(U4{lo.x, lo.y, hi.x, hi.y});
+#pragma unroll
+            for (int j = 0; j < G; ++j)
+                acc[j][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pB[j], acc[j][db], 0, 0, 0);
+        }
+    }
+
+    if (!qvalid) return;
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        float lt = l[j] + xor16(l[j]);
+        lt += xor32(lt);
+        const float inv = __builtin_amdgcn_rcpf(lt);
+        char *orow = p.out + ((int64_t)(t0 + qpos) * p.o_st + (h * G + j) * p.o_sh) * 2;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            const uint2 v = {cvt_pk_bf16_canon(acc[j][db][0] * inv, acc[j][db][1] * inv),
+                             cvt_pk_bf16_canon(acc[j][db][2] * inv, acc[j][db][3] * inv)};
+            *reinterpret_cast<uint2 *>(orow + (16 * db + 4 * g) * 2) = v;
+        }
+    }
+}
+
 }  // namespace q3t
 
 using namespace q3t;
@@ -117,8 +324,54 @@ extern "C" int q3t_prefill_rope_write(const q3t_prefill_rope_write_args *a, void
     return launch_status();
 }
 
+
+template <int D, int G>
+static void launch_prefill(const PrefillParams &p, hipStream_t s) {
+    hipLaunchKernelGGL((prefill_attention_kernel<D, G>), dim3((uint32_t)p.B * p.nqb * p.Hkv), dim3(256), 0, s, p);
+}
+
 extern "C" int q3t_prefill_attention(const q3t_prefill_args *a, void *stream) {
-    (void)a;
-    (void)stream;
-    return Q3T_EUNSUPPORTED;
+    if (!a) return Q3T_EINVAL;
+    if (a->batch < 1 || a->batch > (1 << 20) || a->total_tokens < 0 || a->total_tokens > INT32_MAX ||
+        a->max_seqlen < 0 || a->capacity < 1 || a->q_heads < 1 || a->kv_heads < 1 ||
+        a->q_heads % a->kv_heads)
+        return Q3T_EINVAL;
+    if (a->head_dim != 64 && a->head_dim != 128) return Q3T_EUNSUPPORTED;
+    const int64_t G = a->q_heads / a->kv_heads;
+    if (G != 1 && G != 2 && G != 4) return Q3T_EUNSUPPORTED;
+    if (a->total_tokens == 0 || a->max_seqlen == 0) return Q3T_OK;
+    if (!a->cu_seqlens || !a->query || !a->keys || !a->values || !a->out) return Q3T_EINVAL;
+    const int64_t st[] = {a->q_stride_t, a->q_stride_h, a->k_stride_b, a->k_stride_h, a->k_stride_t,
+                          a->v_stride_b, a->v_stride_h, a->v_stride_t, a->o_stride_t, a->o_stride_h};
+    for (int64_t v : st)
+        if (v < 0 || (v * 2) % 16) return Q3T_EINVAL;
+    if (!aligned(a->query, 16) || !aligned(a->keys, 16) || !aligned(a->values, 16) || !aligned(a->out, 8))
+        return Q3T_EINVAL;
+    // key rows of one (slot, head) are addressed by 32-bit byte offsets
+    const int64_t max_st = a->k_stride_t > a->v_stride_t ? a->k_stride_t : a->v_stride_t;
+    if (a->capacity * max_st * 2 + a->head_dim * 2 > INT32_MAX) return Q3T_EUNSUPPORTED;
+    PrefillParams p;
+    p.B = (int)a->batch; p.Hq = (int)a->q_heads; p.Hkv = (int)a->kv_heads;
+    p.nqb = (int)((a->max_seqlen + kQBlock - 1) / kQBlock);
+    if ((int64_t)p.B * p.nqb * p.Hkv > INT32_MAX) return Q3T_EUNSUPPORTED;
+    p.scale_log2 = a->scale * kLog2eP;
+    p.cu = a->cu_seqlens;
+    p.q = (const char *)a->query; p.q_st = a->q_stride_t; p.q_sh = a->q_stride_h;
+    p.k = (const char *)a->keys; p.v = (const char *)a->values;
+    p.k_sb = a->k_stride_b; p.k_sh = a->k_stride_h; p.k_st = a->k_stride_t;
+    p.v_sb = a->v_stride_b; p.v_sh = a->v_stride_h; p.v_st = a->v_stride_t;
+    p.slots = a->kv_slots;
+    p.cap = a->capacity;
+    p.T = a->total_tokens;
+    p.out = (char *)a->out; p.o_st = a->o_stride_t; p.o_sh = a->o_stride_h;
+    hipStream_t s = (hipStream_t)stream;
+    switch ((a->head_dim == 128 ? 10 : 0) + (int)G) {
+        case 11: launch_prefill<128, 1>(p, s); break;
+        case 12: launch_prefill<128, 2>(p, s); break;
+        case 14: launch_prefill<128, 4>(p, s); break;
+        case 1: launch_prefill<64, 1>(p, s); break;
+        case 2: launch_prefill<64, 2>(p, s); break;
+        default: launch_prefill<64, 4>(p, s); break;
+    }
+    return launch_status();
 }

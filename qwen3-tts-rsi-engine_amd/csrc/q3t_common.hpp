@@ -48,6 +48,8 @@ Q3T_DEVICE float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                            __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
+Q3T_DEVICE float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // DPP lane exchanges within rows of 16 lanes.
 template <int CTRL>
 Q3T_DEVICE float dpp(float x) {
