@@ -51,6 +51,59 @@ def attention_bytes(contexts: torch.Tensor) -> int:
     return (int(contexts.sum()) + BATCH) * HKV * D * 2 * 2 + BATCH * HQ * D * 2 * 2 + BATCH * 8
 
 
+def prefill_detail(pkg, device, reps=20):
+    """The prefill workload: 16 prompts, lengths randint(32, 513, (16,)) under seed 0
+    (sum 4790), 28 layers of RoPE + arena write + varlen causal GQA in one graph.
+    Returns per-layer times and the MFMA rate of the attention kernel."""
+    gen = torch.Generator().manual_seed(0)
+    lengths = torch.randint(32, 513, (16,), generator=gen)
+    total, longest = int(lengths.sum()), int(lengths.max())
+    cu = torch.zeros(17, dtype=torch.int32)
+    cu[1:] = torch.cumsum(lengths, 0)
+    positions = torch.cat([torch.arange(int(n)) for n in lengths]).to(device)
+    dgen = torch.Generator(device=device).manual_seed(2)
+    qkv = torch.randn(LAYERS, total, HQ + 2 * HKV, D, generator=dgen, device=device, dtype=torch.bfloat16)
+    arena = torch.zeros(2 * LAYERS, 16, HKV, 512, D, device=device, dtype=torch.bfloat16)
+    cos, sin = pkg.rope_tables(positions, D)
+    dcu = cu.to(device)
+    out = torch.empty(LAYERS, total, HQ, D, device=device, dtype=torch.bfloat16)
+    q_rot = torch.empty(LAYERS, total, HQ, D, device=device, dtype=torch.bfloat16)
+
+    def step(attention_only):
+        for layer in range(LAYERS):
+            row = qkv[layer]
+            q, k, v = row[:, :HQ], row[:, HQ:HQ + HKV], row[:, HQ + HKV:]
+            if not attention_only:
+                pkg.prefill_rope_write(q, k, v, cos, sin, dcu, arena[layer], arena[LAYERS + layer],
+                                       q_out=q_rot[layer])
+            pkg.prefill_attention(q_rot[layer], arena[layer], arena[LAYERS + layer], dcu, longest,
+                                  out=out[layer])
+
+    times = {}
+    for attention_only in (False, True):
+        step(attention_only)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step(attention_only)
+        graph.replay()
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            graph.replay()
+        stop.record()
+        torch.cuda.synchronize()
+        times[attention_only] = start.elapsed_time(stop) * 1e3 / (reps * LAYERS)
+    flops = 2 * D * HQ * int((lengths * (lengths + 1)).sum())
+    return {"workload": "16 prompts, lengths randint(32,513) seed 0, sum %d, 28 layers" % total,
+            "us_per_layer_rope_write_attention": times[False],
+            "us_per_layer_attention": times[True],
+            "attention_flops_per_layer": flops,
+            "attention_TFLOPs": flops / (times[True] * 1e-6) / 1e12,
+            "mfma_frac_of_2500_TFLOPs": flops / (times[True] * 1e-6) / 2.5e15}
+
+
 def read_traffic():
     """HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (committed summary)."""
     if not TRAFFIC_SUMMARY.exists():
@@ -192,6 +245,7 @@ def main():
                 raise RuntimeError("calibration copy failed")
         torch.cuda.synchronize()
 
+    prefill = prefill_detail(pkg, device)
     traffic = read_traffic()
     result = {
         "metric": "decode-attn tokens/s + achieved HBM GB/s, 64-req ragged talker step, 1 GPU",
@@ -220,7 +274,8 @@ def main():
                    "us_per_layer_attention_only": attn_us,
                    "attention_only_GBs": attention_bytes(contexts) / (attn_us * 1e-6) / 1e9,
                    "max_chunks": args.max_chunks,
-                   "wall_s_timed_region": wall},
+                   "wall_s_timed_region": wall,
+                   "prefill": prefill},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

@@ -22,11 +22,16 @@ from .kv_write import write, write_tokens
 from .rotary import rotary, rope_tables, inverse_frequencies
 from .attention import attention, decode_attention, decode_step, prefill_attention
 from .prefill import prefill_rope_write, prefill_step
+from .packed_attention import PackedAttention, install_packed_attention, restore_modules
+from .scheduler import SlotScheduler, DecodeBatch
+from .slots import SlotArena, SlotCache, PredictorCache, grow_arena
 
 __all__ = [
     "decode_batch_size", "copy_packed_prefix", "copy_rows", "write", "write_tokens", "rotary",
     "rope_tables", "inverse_frequencies", "attention", "decode_attention", "decode_step",
-    "prefill_attention", "prefill_rope_write", "prefill_step", "library",
+    "prefill_attention", "prefill_rope_write", "prefill_step", "PackedAttention",
+    "install_packed_attention", "restore_modules", "SlotScheduler", "DecodeBatch", "SlotArena",
+    "SlotCache", "PredictorCache", "grow_arena", "library",
 ]
 
 library = _lib.library

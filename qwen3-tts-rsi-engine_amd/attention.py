@@ -181,6 +181,22 @@ def decode_step(query, new_key, new_value, key_arena, value_arena, positions, co
     return out
 
 
+_LENGTH_POSITIONS: dict = {}
+
+
+def _length_positions(lengths, device):
+    """Device positions n - 1 for a list of key counts, cached: captured graphs keep using
+    the same tensor, and no host copy happens during capture."""
+    key = (tuple(int(n) for n in lengths), device)
+    cached = _LENGTH_POSITIONS.get(key)
+    if cached is None:
+        if torch.cuda.is_current_stream_capturing():
+            raise ValueError('actual_seq_lengths_kv must be seen once before graph capture')
+        cached = torch.tensor([n - 1 for n in key[0]], device=device, dtype=torch.int64)
+        _LENGTH_POSITIONS[key] = cached
+    return cached
+
+
 def attention(module, query, key, value, attention_mask, **kwargs):
     """Drop-in for the reference's native GQA call: query (B, Hq, S, D), key/value
     (B, Hkv, ctx, D) BNSD; returns ((B, S, Hq, D) contiguous, None).
@@ -198,12 +214,15 @@ def attention(module, query, key, value, attention_mask, **kwargs):
     positions = kwargs.get('kv_positions')
     lengths = kwargs.get('actual_seq_lengths_kv')
     device = query.device
+    mask = attention_mask
     if positions is None:
         if lengths is not None:
-            positions = torch.tensor([int(n) - 1 for n in lengths], device=device, dtype=torch.int64)
+            positions = _length_positions(lengths, device)
         else:
             positions = torch.full((batch,), ctx - 1, device=device, dtype=torch.int64)
-    mask = attention_mask
+        if mask is None and 1 < qlen <= 2 and getattr(module, 'is_causal', True):
+            # the reference operator's default for several queries: query i sees keys 0 ... i
+            mask = torch.ones(qlen, ctx, device=device, dtype=torch.bool).tril()
     if mask is not None and qlen > 2:
         raise ValueError('explicit masks are supported for query lengths up to 2; '
                          'use prefill_attention for causal prefill')

@@ -1,0 +1,149 @@
+"""Drop-in ``PackedAttention`` for the Qwen3-TTS attention modules on the package's kernels.
+
+Same plug-in mechanism as the reference (qwen3_tts_engine/packed_attention.py:11-95,
+operators.py:36-38): ``install_packed_attention`` swaps every child whose class is named
+``Qwen3TTSTalkerAttention`` or ``Qwen3TTSAttention`` for a ``PackedAttention`` wrapping it
+and returns ``(parent, name, original)`` tuples for ``restore_modules``.  The constructor
+takes the reference's flags with the same validation.
+
+Forward, as the reference: one fused QKV projection, the module's own q/k RMSNorm, rotary
+embedding, cache update, attention, o_proj.  Rotary and attention always run on the HIP
+kernels (the flags that select the reference's Ascend operators are accepted for
+signature compatibility):
+
+* a one-token bf16 step over a ``SlotCache`` is a single ``decode_step`` launch: RoPE of q
+  and k, the paired K/V write at the cache positions and ragged GQA attention over keys
+  0 ... position (the ``j <= pos[b]`` mask of SlotGraph.compute, continuous.py:191-192,
+  which the reference adds as 0 / finfo.min);
+* every other call rotates q/k with ``rotary`` (bf16-exact to torch eager), lets the cache
+  update and calls ``attention`` (the npu_attention.attention drop-in).
+"""
+from __future__ import annotations
+
+import torch
+
+from .attention import attention, decode_step
+from .rotary import rotary
+from .slots import SlotCache
+
+_ATTENTION_CLASSES = ('Qwen3TTSTalkerAttention', 'Qwen3TTSAttention')
+
+
+def _section_axes(head_dim, sections, interleaved, device):
+    """Per-dimension axis (0 temporal, 1 height, 2 width) of a sectioned multimodal RoPE:
+    consecutive sections of each half, or frequency f -> f % 3 when interleaved."""
+    half = head_dim // 2
+    if interleaved:
+        axes = [f % 3 for f in range(half)]
+    else:
+        axes = [i % 3 for i, n in enumerate(sections) for _ in range(n)]
+    if len(axes) != half:
+        raise ValueError('mrope sections must cover half of head_dim')
+    return torch.tensor(axes + axes, device=device, dtype=torch.int64)
+
+
+class PackedAttention(torch.nn.Module):
+    def __init__(self, reference, native_gqa=False, text_only_rope=False, reference_single=False,
+                 native_rope=False, native_rope_scope="all", triton_talker_rope=False):
+        super().__init__()
+        self.reference = reference
+        projections = [reference.q_proj, reference.k_proj, reference.v_proj]
+        self.sizes = [projection.out_features for projection in projections]
+        self.weight = torch.nn.Parameter(torch.cat([p.weight.detach() for p in projections], dim=0),
+                                         requires_grad=False)
+        self.bias = None
+        if projections[0].bias is not None:
+            self.bias = torch.nn.Parameter(torch.cat([p.bias.detach() for p in projections], dim=0),
+                                           requires_grad=False)
+        self.multimodal = reference.__class__.__name__ == 'Qwen3TTSTalkerAttention'
+        if native_rope_scope not in ('all', 'talker', 'predictor'):
+            raise ValueError('Native rotary scope must be all, talker or predictor')
+        self.native_rope = native_rope and (native_rope_scope == 'all'
+                                            or (native_rope_scope == 'talker') == self.multimodal)
+        if native_rope and self.multimodal and not text_only_rope:
+            raise ValueError("Native rotary requires identical CustomVoice position axes")
+        self.triton_talker_rope = triton_talker_rope and self.multimodal
+        if self.triton_talker_rope and not text_only_rope:
+            raise ValueError("Triton talker rotary requires identical CustomVoice position axes")
+        self.native_gqa = native_gqa
+        self.reference_single = reference_single
+        self.text_only_rope = text_only_rope
+        self._axes = None
+
+    def _tables(self, position_embeddings, batch, length):
+        """cos/sin as contiguous (batch, length, head_dim) rows."""
+        cos, sin = position_embeddings
+        if self.multimodal:
+            if self.text_only_rope:
+                cos, sin = cos[0], sin[0]
+            else:
+                scaling = self.reference.rope_scaling
+                if self._axes is None or self._axes.device != cos.device:
+                    self._axes = _section_axes(cos.shape[-1], scaling['mrope_section'],
+                                               scaling.get('interleaved', False), cos.device)
+                index = self._axes.view(1, 1, 1, -1).expand(1, *cos.shape[1:])
+                cos, sin = cos.gather(0, index)[0], sin.gather(0, index)[0]
+        cos = cos.expand(batch, length, cos.shape[-1]).contiguous()
+        sin = sin.expand(batch, length, sin.shape[-1]).contiguous()
+        return cos, sin
+
+    def forward(self, hidden_states, position_embeddings, attention_mask, past_key_values=None,
+                cache_position=None, **kwargs):
+        reference = self.reference
+        shape = hidden_states.shape[:-1]
+        batch, length = shape[0], shape[1]
+        heads = (*shape, -1, reference.head_dim)
+        projected = torch.nn.functional.linear(hidden_states, self.weight, self.bias)
+        query, key, value = projected.split(self.sizes, dim=-1)
+        query = reference.q_norm(query.reshape(heads))     # BSND
+        key = reference.k_norm(key.reshape(heads))
+        value = value.reshape(heads)
+        cos, sin = self._tables(position_embeddings, batch, length)
+
+        if (isinstance(past_key_values, SlotCache) and length == 1 and not reference.training
+                and query.dtype == torch.bfloat16 and reference.head_dim == 128
+                and past_key_values.arena.keys[reference.layer_idx].is_contiguous()):
+            arena = past_key_values.arena
+            output = decode_step(query, key, value, arena.keys[reference.layer_idx],
+                                 arena.values[reference.layer_idx], past_key_values.positions,
+                                 cos[:, 0], sin[:, 0], scale=reference.scaling)
+            return reference.o_proj(output.reshape(*shape, -1)), None
+
+        query = rotary(query.contiguous(), cos, sin).transpose(1, 2)
+        key = rotary(key.contiguous(), cos, sin).transpose(1, 2)
+        value = value.transpose(1, 2)
+        if past_key_values is not None:
+            key, value = past_key_values.update(key, value, reference.layer_idx,
+                                                {'sin': sin, 'cos': cos, 'cache_position': cache_position})
+        if isinstance(past_key_values, SlotCache):
+            kwargs['kv_positions'] = past_key_values.positions
+        else:
+            lengths = getattr(past_key_values, 'actual_seq_lengths_kv', None)
+            if lengths is not None:
+                kwargs['actual_seq_lengths_kv'] = lengths
+        output, weights = attention(reference, query, key, value, attention_mask,
+                                    dropout=0.0 if not reference.training else reference.attention_dropout,
+                                    scaling=reference.scaling, sliding_window=reference.sliding_window,
+                                    **kwargs)
+        return reference.o_proj(output.reshape(*shape, -1).contiguous()), weights
+
+
+def install_packed_attention(model, native_gqa=False, text_only_rope=False, reference_single=False,
+                             native_rope=False, native_rope_scope="all", triton_talker_rope=False):
+    """Swap every Qwen3-TTS attention module of ``model`` for a PackedAttention."""
+    replacements = []
+    for parent in list(model.modules()):
+        for name, child in list(parent.named_children()):
+            if child.__class__.__name__ in _ATTENTION_CLASSES:
+                replacements.append((parent, name, child))
+                setattr(parent, name, PackedAttention(
+                    child, native_gqa=native_gqa, text_only_rope=text_only_rope,
+                    reference_single=reference_single, native_rope=native_rope,
+                    native_rope_scope=native_rope_scope, triton_talker_rope=triton_talker_rope))
+    return replacements
+
+
+def restore_modules(replacements):
+    """Undo install_packed_attention (latest replacement first)."""
+    for parent, name, original in reversed(replacements):
+        setattr(parent, name, original)
