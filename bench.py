@@ -104,6 +104,55 @@ def prefill_detail(pkg, device, reps=20):
             "mfma_frac_of_2500_TFLOPs": flops / (times[True] * 1e-6) / 2.5e15}
 
 
+def predictor_detail(pkg, device, reps=20):
+    """The code predictor's attention: 64 requests, 5 layers, 15 steps over a 16-position
+    cache (PredictorCache windows: step 0 writes positions 0-1 and attends them causally,
+    step s writes s+1 and attends 0..s+1).  Step 0 is the two-token write + masked-causal
+    decode; steps 1-14 are fused one-token launches.  All 75 layer-steps in one graph."""
+    layers, steps, batch, cap = 5, 15, BATCH, 16
+    dgen = torch.Generator(device=device).manual_seed(3)
+    arena = torch.zeros(2 * layers, batch, HKV, cap, D, device=device, dtype=torch.bfloat16)
+    rows = torch.randn(steps, layers, batch, 2, HQ + 2 * HKV, D, generator=dgen, device=device,
+                       dtype=torch.bfloat16)
+    positions = [torch.full((batch,), max(s + 1, 1), device=device, dtype=torch.int64) for s in range(steps)]
+    start0 = torch.zeros(batch, device=device, dtype=torch.int64)
+    tables = [pkg.rope_tables(positions[s], D) for s in range(steps)]
+    cos0, sin0 = pkg.rope_tables(torch.arange(2, device=device).expand(batch, 2).contiguous(), D)
+    out = torch.empty(batch, 2, HQ, D, device=device, dtype=torch.bfloat16)
+
+    def chain():
+        for s in range(steps):
+            for layer in range(layers):
+                r = rows[s, layer]
+                keys, values = arena[layer], arena[layers + layer]
+                if s == 0:
+                    q = pkg.rotary(r[:, :, :HQ].contiguous(), cos0, sin0)
+                    k = pkg.rotary(r[:, :, HQ:HQ + HKV].contiguous(), cos0, sin0)
+                    pkg.write_tokens(k.transpose(1, 2), r[:, :, HQ + HKV:].transpose(1, 2), keys, values, start0)
+                    pkg.decode_attention(q, keys, values, positions[0], out=out)
+                else:
+                    q, k, v = r[:, :1, :HQ], r[:, :1, HQ:HQ + HKV], r[:, :1, HQ + HKV:]
+                    pkg.decode_step(q, k, v, keys, values, positions[s], *tables[s], out=out[:, :1])
+
+    chain()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        chain()
+    graph.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    chain_us = start.elapsed_time(stop) * 1e3 / reps
+    return {"workload": "code predictor: 64 requests, 5 layers, 15 steps, 16-position cache",
+            "us_per_15_step_chain": chain_us, "us_per_step": chain_us / steps,
+            "us_per_layer_step": chain_us / (steps * layers)}
+
+
 def read_traffic():
     """HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (committed summary)."""
     if not TRAFFIC_SUMMARY.exists():
@@ -113,11 +162,14 @@ def read_traffic():
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(seconds: float):
+def cpu_baseline(seconds: float, threads: int = 0):
     """The reference's torch decode layer (scatter_ write, eager bf16 RoPE, SDPA under the
     0/finfo.min context mask) on this host, one layer of the same 64-request workload."""
     from oracle import torch_path
 
+    previous = torch.get_num_threads()
+    if threads:
+        torch.set_num_threads(threads)
     threads = torch.get_num_threads()
     gen = torch.Generator().manual_seed(0)
     contexts = torch.randint(64, 1025, (BATCH,), generator=gen)
@@ -142,11 +194,12 @@ def cpu_baseline(seconds: float):
                 break
     times.sort()
     layer_s = times[len(times) // 2]
+    torch.set_num_threads(previous)
     return {"value": BATCH / (LAYERS * layer_s), "unit": "tokens/s", "cores": threads,
             "kind": "port",
             "sample": (f"median of {len(times)} runs of one talker layer (64 requests, capacity "
-                       f"{CAPACITY}, bf16, torch {threads} threads) = {layer_s * 1e3:.2f} ms, "
-                       f"scaled to a 28-layer step")}
+                       f"{CAPACITY}, bf16, torch {threads} threads, {len(os.sched_getaffinity(0))} "
+                       f"cores in the affinity mask) = {layer_s * 1e3:.2f} ms, scaled to a 28-layer step")}
 
 
 def main():
@@ -246,6 +299,7 @@ def main():
         torch.cuda.synchronize()
 
     prefill = prefill_detail(pkg, device)
+    predictor = predictor_detail(pkg, device)
     traffic = read_traffic()
     result = {
         "metric": "decode-attn tokens/s + achieved HBM GB/s, 64-req ragged talker step, 1 GPU",
@@ -275,10 +329,14 @@ def main():
                    "attention_only_GBs": attention_bytes(contexts) / (attn_us * 1e-6) / 1e9,
                    "max_chunks": args.max_chunks,
                    "wall_s_timed_region": wall,
-                   "prefill": prefill},
+                   "prefill": prefill,
+                   "predictor": predictor},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        # the reference pins torch to 4 threads (model.py:16); reported beside the all-core figure
+        four = cpu_baseline(args.cpu_seconds / 2, threads=4)
+        result["detail"]["cpu_baseline_4_threads"] = {"value": four["value"], "sample": four["sample"]}
     print(json.dumps(result), flush=True)
 
 
