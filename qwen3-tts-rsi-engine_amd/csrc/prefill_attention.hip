@@ -92,7 +92,8 @@ __global__ void __launch_bounds__(256) prefill_rope_write_kernel(PrefillRopeWrit
 // Each lane therefore keeps the online-softmax state of one query per head, with no data
 // movement between the two products.
 constexpr int kQBlock = 64;
-constexpr int kKTile = 32;
+constexpr int kKTile = 32;   // keys staged per barrier pair
+constexpr int kKSub = 32;    // keys per product step
 constexpr float kLog2eP = 1.4426950408889634f;
 constexpr float kEmptyP = -1.0e30f;
 
@@ -121,7 +122,7 @@ __global__ void __launch_bounds__(256) prefill_attention_kernel(PrefillParams p)
     constexpr int KK = D / 32;   // MFMA steps over the head dimension
     constexpr int DB = D / 16;   // 16-row blocks of O^T
     constexpr int KROW = D + 8;  // padded LDS row of K (bf16)
-    constexpr int VROW = kKTile + 4;
+    constexpr int VROW = kKTile + 2;  // 4-byte rows: the transposed writes of 16 lanes spread over 8 banks
     constexpr int CPR = D / 8;   // 16-byte chunks per row
     __shared__ uint16_t sK[kKTile][KROW];
     __shared__ uint16_t sVt[D][VROW];
@@ -204,31 +205,35 @@ __global__ void __launch_bounds__(256) prefill_attention_kernel(PrefillParams p)
         stage();
         __syncthreads();
         if (kt + 1 < ntiles) fetch(kt + 1);  // in flight during this tile's products
-        const int kbase_idx = kt * kKTile;
-        if (kbase_idx > q0 + 16 * wave + 15) continue;  // the whole tile is above this wave's diagonal
-
-        // S^T for both 16-key halves of the tile and every head
-        f32x4_t st[2][G];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+        for (int sub = 0; sub < kKTile / kKSub; ++sub) {
+        const int kbase_idx = kt * kKTile + sub * kKSub;
+        if (kbase_idx > q0 + 16 * wave + 15) break;  // the rest of the tile is above this wave's diagonal
+
+        // S^T for the 16-key blocks of the tile and every head
+        constexpr int NKB = kKSub / 16;
+        f32x4_t st[NKB][G];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
             for (int j = 0; j < G; ++j) st[kb][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kk = 0; kk < KK; ++kk) {
-                const bf16x8_t a = as_bf16x8(*reinterpret_cast<const U4 *>(&sK[16 * kb + c][32 * kk + 8 * g]));
+                const bf16x8_t a = as_bf16x8(*reinterpret_cast<const U4 *>(&sK[sub * kKSub + 16 * kb + c][32 * kk + 8 * g]));
 #pragma unroll
                 for (int j = 0; j < G; ++j)
                     st[kb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qB[j][kk], st[kb][j], 0, 0, 0);
             }
         }
-        // scale, causal mask, online softmax per (head, query c); P^T packed to bf16
-        bf16x8_t pB[G];
+        // scale, causal mask, online softmax per (head, query c); P^T packed to bf16, one
+        // B operand per 32 keys (blocks 2s and 2s+1)
+        bf16x8_t pB[NKB / 2][G];
 #pragma unroll
         for (int j = 0; j < G; ++j) {
-            float x[8];
+            float x[NKB * 4];
             float mx = kEmptyP;
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int key = kbase_idx + 16 * kb + 4 * g + i;
@@ -242,28 +247,36 @@ __global__ void __launch_bounds__(256) prefill_attention_kernel(PrefillParams p)
             const float alpha = fexp2(m[j] - mn);
             m[j] = mn;
             float ps = 0.f;
-            float pv[8];
+            float pv[NKB * 4];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
+            for (int e = 0; e < NKB * 4; ++e) {
                 pv[e] = fexp2(x[e] - mn);
                 ps += pv[e];
             }
             l[j] = l[j] * alpha + ps;  // this lane's keys only; summed over g at the end
 #pragma unroll
             for (int db = 0; db < DB; ++db) acc[j][db] *= alpha;
-            const U4 packed = {cvt_pk_bf16(pv[0], pv[1]), cvt_pk_bf16(pv[2], pv[3]),
-                               cvt_pk_bf16(pv[4], pv[5]), cvt_pk_bf16(pv[6], pv[7])};
-            pB[j] = as_bf16x8(packed);
+#pragma unroll
+            for (int sp = 0; sp < NKB / 2; ++sp) {
+                const float *q8 = pv + 8 * sp;
+                const U4 packed = {cvt_pk_bf16(q8[0], q8[1]), cvt_pk_bf16(q8[2], q8[3]),
+                                   cvt_pk_bf16(q8[4], q8[5]), cvt_pk_bf16(q8[6], q8[7])};
+                pB[sp][j] = as_bf16x8(packed);
+            }
         }
-        // O^T += V^T . P^T
+        // O^T += V^T . P^T, 32 keys per product
 #pragma unroll
-        for (int db = 0; db < DB; ++db) {
-            const uint2 lo = *reinterpret_cast<const uint2 *>(&sVt[16 * db + c][4 * g]);
-            const uint2 hi = *reinterpret_cast<const uint2 *>(&sVt[16 * db + c][16 + 4 * g]);
-            const bf16x8_t a = as_bf16x8(U4{lo.x, lo.y, hi.x, hi.y});
+        for (int sp = 0; sp < NKB / 2; ++sp) {
 #pragma unroll
-            for (int j = 0; j < G; ++j)
-                acc[j][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pB[j], acc[j][db], 0, 0, 0);
+            for (int db = 0; db < DB; ++db) {
+                const uint32_t *row = reinterpret_cast<const uint32_t *>(&sVt[16 * db + c][0]);
+                const int k0 = (sub * kKSub + 32 * sp + 4 * g) / 2, k1 = (sub * kKSub + 32 * sp + 16 + 4 * g) / 2;
+                const bf16x8_t a = as_bf16x8(U4{row[k0], row[k0 + 1], row[k1], row[k1 + 1]});
+#pragma unroll
+                for (int j = 0; j < G; ++j)
+                    acc[j][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pB[sp][j], acc[j][db], 0, 0, 0);
+            }
+        }
         }
     }
 
