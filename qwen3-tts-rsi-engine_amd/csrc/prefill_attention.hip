@@ -79,10 +79,12 @@ __global__ void __launch_bounds__(256) prefill_rope_write_kernel(PrefillRopeWrit
 
 // ---- varlen causal attention on bf16 MFMA tiles ------------------------------------------
 //
-// One workgroup of 4 waves per (request, 64-query block, KV head); wave w owns queries
-// q0 + 16w ... q0 + 16w + 15 of all G query heads that share the KV head.  Keys stream in
-// tiles of 32 through LDS: K row-major, V transposed, so that both products read 16-byte
-// (K) or 8-byte (V) runs.  With v_mfma_f32_16x16x32_bf16 (lane l = 16g + c holds
+// One workgroup of 4 waves per (request, 64-query block, G query heads of one KV head);
+// wave w owns queries q0 + 16w ... q0 + 16w + 15.  The launch uses G = 1 (one query head
+// per workgroup: fewer accumulators, three workgroups per CU).  Keys stream in tiles of 32
+// through LDS: K row-major, V transposed (rows padded to 4-byte multiples so that the
+// transposed writes spread over 8 banks), so that both products read 16-byte (K) or 4-byte
+// (V) runs.  With v_mfma_f32_16x16x32_bf16 (lane l = 16g + c holds
 // A[c][8g..8g+7], B[8g..8g+7][c] and D[4g..4g+3][c]):
 //   S^T (keys x queries) = K . Q^T   A = K rows from LDS, B = the wave's Q rows (registers);
 //                                    lane (g, c) gets keys 4g..4g+3 of query c per 16 keys;
@@ -101,7 +103,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 struct PrefillParams {
-    int B, Hq, Hkv, nqb;
+    int B, Hq, Hkv, nqb, group;
     int64_t T;
     float scale_log2;
     const int32_t *cu;
@@ -119,6 +121,7 @@ Q3T_DEVICE bf16x8_t as_bf16x8(const U4 &v) { return __builtin_bit_cast(bf16x8_t,
 
 template <int D, int G>
 __global__ void __launch_bounds__(256) prefill_attention_kernel(PrefillParams p) {
+    // G: query heads per workgroup (a divisor of the GQA group p.group)
     constexpr int KK = D / 32;   // MFMA steps over the head dimension
     constexpr int DB = D / 16;   // 16-row blocks of O^T
     constexpr int KROW = D + 8;  // padded LDS row of K (bf16)
@@ -129,8 +132,10 @@ __global__ void __launch_bounds__(256) prefill_attention_kernel(PrefillParams p)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
-    const int h = blockIdx.x % p.Hkv;
-    const int rest = blockIdx.x / p.Hkv;
+    const int hgroups = p.Hq / G;
+    const int hq0 = (blockIdx.x % hgroups) * G;  // first query head of this workgroup
+    const int h = hq0 / p.group;                  // its KV head
+    const int rest = blockIdx.x / hgroups;
     const int b = rest % p.B;
     const int qb = p.nqb - 1 - rest / p.B;  // the longest blocks are dispatched first
     const int t0 = p.cu[b];
@@ -149,7 +154,7 @@ __global__ void __launch_bounds__(256) prefill_attention_kernel(PrefillParams p)
     bf16x8_t qB[G][KK];
 #pragma unroll
     for (int j = 0; j < G; ++j) {
-        const char *row = p.q + ((int64_t)(t0 + (qvalid ? qpos : 0)) * p.q_st + (h * G + j) * p.q_sh) * 2;
+        const char *row = p.q + ((int64_t)(t0 + (qvalid ? qpos : 0)) * p.q_st + (hq0 + j) * p.q_sh) * 2;
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
             U4 v = load16(row + (32 * kk + 8 * g) * 2);
@@ -286,7 +291,7 @@ __global__ void __launch_bounds__(256) prefill_attention_kernel(PrefillParams p)
         float lt = l[j] + xor16(l[j]);
         lt += xor32(lt);
         const float inv = __builtin_amdgcn_rcpf(lt);
-        char *orow = p.out + ((int64_t)(t0 + qpos) * p.o_st + (h * G + j) * p.o_sh) * 2;
+        char *orow = p.out + ((int64_t)(t0 + qpos) * p.o_st + (hq0 + j) * p.o_sh) * 2;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
             const uint2 v = {cvt_pk_bf16_canon(acc[j][db][0] * inv, acc[j][db][1] * inv),
@@ -340,7 +345,7 @@ extern "C" int q3t_prefill_rope_write(const q3t_prefill_rope_write_args *a, void
 
 template <int D, int G>
 static void launch_prefill(const PrefillParams &p, hipStream_t s) {
-    hipLaunchKernelGGL((prefill_attention_kernel<D, G>), dim3((uint32_t)p.B * p.nqb * p.Hkv), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((prefill_attention_kernel<D, G>), dim3((uint32_t)p.B * p.nqb * (p.Hq / G)), dim3(256), 0, s, p);
 }
 
 extern "C" int q3t_prefill_attention(const q3t_prefill_args *a, void *stream) {
@@ -365,8 +370,9 @@ extern "C" int q3t_prefill_attention(const q3t_prefill_args *a, void *stream) {
     if (a->capacity * max_st * 2 + a->head_dim * 2 > INT32_MAX) return Q3T_EUNSUPPORTED;
     PrefillParams p;
     p.B = (int)a->batch; p.Hq = (int)a->q_heads; p.Hkv = (int)a->kv_heads;
+    p.group = (int)G;
     p.nqb = (int)((a->max_seqlen + kQBlock - 1) / kQBlock);
-    if ((int64_t)p.B * p.nqb * p.Hkv > INT32_MAX) return Q3T_EUNSUPPORTED;
+    if ((int64_t)p.B * p.nqb * p.Hq > INT32_MAX) return Q3T_EUNSUPPORTED;
     p.scale_log2 = a->scale * kLog2eP;
     p.cu = a->cu_seqlens;
     p.q = (const char *)a->query; p.q_st = a->q_stride_t; p.q_sh = a->q_stride_h;
@@ -378,13 +384,9 @@ extern "C" int q3t_prefill_attention(const q3t_prefill_args *a, void *stream) {
     p.T = a->total_tokens;
     p.out = (char *)a->out; p.o_st = a->o_stride_t; p.o_sh = a->o_stride_h;
     hipStream_t s = (hipStream_t)stream;
-    switch ((a->head_dim == 128 ? 10 : 0) + (int)G) {
-        case 11: launch_prefill<128, 1>(p, s); break;
-        case 12: launch_prefill<128, 2>(p, s); break;
-        case 14: launch_prefill<128, 4>(p, s); break;
-        case 1: launch_prefill<64, 1>(p, s); break;
-        case 2: launch_prefill<64, 2>(p, s); break;
-        default: launch_prefill<64, 4>(p, s); break;
-    }
+    // one query head per workgroup: the accumulators of a single head keep the kernel at a
+    // register count that leaves two workgroups per CU's SIMDs busy
+    if (a->head_dim == 128) launch_prefill<128, 1>(p, s);
+    else launch_prefill<64, 1>(p, s);
     return launch_status();
 }
