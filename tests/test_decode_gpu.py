@@ -300,3 +300,65 @@ def test_split_merge_is_deterministic_across_launches(pkg, device, kv_heads, max
         assert torch.equal(again, first)
     expected = oatt.decode_attention(f64(q), f64(k), f64(v), contexts.numpy(), D ** -0.5)
     assert_attention_close(f64(first), expected)
+
+
+def test_maximum_batch(pkg, device):
+    """1024 requests (the largest batch), short contexts including position 0."""
+    batch, capacity = 1024, 64
+    gen = torch.Generator().manual_seed(70)
+    contexts = torch.randint(0, capacity, (batch,), generator=gen)
+    contexts[:3] = torch.tensor([0, 1, capacity - 1])
+    k, v = _arena(batch, capacity, torch.bfloat16, device, 71)
+    q = torch.randn(batch, 1, HQ, D, generator=gen).bfloat16().to(device)
+    out = pkg.decode_attention(q, k, v, contexts.to(device))
+    expected = oatt.decode_attention(f64(q), f64(k), f64(v), contexts.numpy(), D ** -0.5)
+    assert_attention_close(f64(out), expected)
+
+
+@pytest.mark.parametrize("max_chunks", [0, 3])
+def test_long_context_multi_block_chunks(pkg, device, max_chunks):
+    """An 8192-key arena: with max_chunks 3 every chunk spans many 64-key blocks."""
+    capacity = 8192
+    contexts = torch.tensor([8191, 3000, 64, 0])
+    k, v = _arena(4, capacity, torch.bfloat16, device, 72)
+    gen = torch.Generator().manual_seed(73)
+    q = torch.randn(4, 1, HQ, D, generator=gen).bfloat16().to(device)
+    out = pkg.decode_attention(q, k, v, contexts.to(device), max_chunks=max_chunks)
+    expected = oatt.decode_attention(f64(q), f64(k), f64(v), contexts.numpy(), D ** -0.5)
+    assert_attention_close(f64(out), expected)
+
+
+def test_kv_offsets_address_any_layout(pkg, device):
+    """kv_offsets place each request's rows at an arbitrary element offset of one buffer
+    (a request's keys at offset_b + h * stride_h + j * stride_t)."""
+    batch, capacity = 6, 96
+    gen = torch.Generator().manual_seed(74)
+    flat_k = torch.randn(10 * HKV * capacity * D, generator=gen).bfloat16().to(device)
+    flat_v = torch.randn(10 * HKV * capacity * D, generator=gen).bfloat16().to(device)
+    slots = torch.tensor([9, 2, 5, 0, 7, 3])
+    plane = HKV * capacity * D
+    offsets = (slots * plane).to(device)
+    keys = flat_k.view(10, HKV, capacity, D)
+    values = flat_v.view(10, HKV, capacity, D)
+    contexts = torch.tensor([95, 10, 40, 0, 63, 77])
+    q = torch.randn(batch, 1, HQ, D, generator=gen).bfloat16().to(device)
+    out = pkg.decode_attention(q, keys[:batch], values[:batch], contexts.to(device), kv_offsets=offsets)
+    expected = oatt.decode_attention(f64(q), f64(keys[slots]), f64(values[slots]), contexts.numpy(), D ** -0.5)
+    assert_attention_close(f64(out), expected)
+
+
+def test_fused_step_at_position_zero(pkg, device):
+    """A request at position 0 attends only its own new key: the output is the new value."""
+    batch, capacity = 3, 32
+    k, v = _arena(batch, capacity, torch.bfloat16, device, 75)
+    gen = torch.Generator().manual_seed(76)
+    qkv = torch.randn(batch, 1, (HQ + 2 * HKV) * D, generator=gen).bfloat16().to(device)
+    q = qkv[..., :HQ * D].view(batch, 1, HQ, D)
+    kn = qkv[..., HQ * D:(HQ + HKV) * D].view(batch, 1, HKV, D)
+    vn = qkv[..., (HQ + HKV) * D:].view(batch, 1, HKV, D)
+    positions = torch.zeros(batch, dtype=torch.int64, device=device)
+    cos, sin = pkg.rope_tables(positions, D)
+    out = pkg.decode_step(q, kn, vn, k, v, positions, cos, sin)
+    expected = vn.float().repeat_interleave(HQ // HKV, dim=2)
+    assert torch.allclose(out.float(), expected, atol=1e-2, rtol=1e-2)
+    assert torch.equal(v[:, :, 0], vn[:, 0])
