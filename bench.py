@@ -214,6 +214,9 @@ def main():
     parser.add_argument("--calibrate-bytes", type=int, default=0,
                         help="after timing, launch the plain copy kernel on this many bytes "
                              "(HBM counter calibration under rocprofv3)")
+    parser.add_argument("--prefill-only", action="store_true",
+                        help="run only the prefill workload and print its detail line "
+                             "(for per-kernel profiling of the prefill kernels)")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -223,6 +226,9 @@ def main():
     pkg = __graft_entry__.import_package()
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    if args.prefill_only:
+        print(json.dumps({"prefill": prefill_detail(pkg, device)}), flush=True)
+        return
     gen = torch.Generator().manual_seed(0)
     contexts = torch.randint(64, 1025, (BATCH,), generator=gen)
     positions = contexts.to(device)

@@ -79,28 +79,37 @@ __global__ void __launch_bounds__(256) prefill_rope_write_kernel(PrefillRopeWrit
 
 // ---- varlen causal attention on bf16 MFMA tiles ------------------------------------------
 //
-// One workgroup of 4 waves per (request, 64-query block, G query heads of one KV head);
-// wave w owns queries q0 + 16w ... q0 + 16w + 15.  The launch uses G = 1 (one query head
-// per workgroup: fewer accumulators, three workgroups per CU).  Keys stream in tiles of 32
-// through LDS: K row-major, V transposed (rows padded to 4-byte multiples so that the
-// transposed writes spread over 8 banks), so that both products read 16-byte (K) or 4-byte
-// (V) runs.  With v_mfma_f32_16x16x32_bf16 (lane l = 16g + c holds
-// A[c][8g..8g+7], B[8g..8g+7][c] and D[4g..4g+3][c]):
+// One workgroup per (request, 64-query block, GH query heads of one KV head), 4 waves per
+// query head; wave w of a head owns queries q0 + 16w ... q0 + 16w + 15.  Keys stream through
+// a ring of kStages LDS stages of kTile keys (K rows then V rows), filled by buffer loads
+// that write LDS directly (16 bytes per lane) kStages - 1 tiles ahead of the products, so
+// the K/V reads never pass through registers.  Rows are stored unpadded with their 16-byte
+// chunks XOR-swizzled (K chunk ch of row r at ch ^ (r & 15), V at ch ^ (2r & 15)), which
+// keeps the 16-byte K reads of 16 rows and the transposing 8-byte V reads of 8 rows on
+// distinct banks.  With v_mfma_f32_16x16x32_bf16 (lane l = 16g + c holds A[c][8g..8g+7],
+// B[8g..8g+7][c] and D[4g..4g+3][c]), per 32 keys:
 //   S^T (keys x queries) = K . Q^T   A = K rows from LDS, B = the wave's Q rows (registers);
-//                                    lane (g, c) gets keys 4g..4g+3 of query c per 16 keys;
-//   O^T (dims x queries) += V^T . P^T   B = P^T straight from the S^T registers, its K index
-//                                    ordering keys {4g..4g+3, 16+4g..16+4g+3}; A = V^T rows
-//                                    read from LDS in that same key order.
-// Each lane therefore keeps the online-softmax state of one query per head, with no data
-// movement between the two products.
+//                                    lane (g, c) gets keys 4g..4g+3 and 16+4g..16+4g+3 of
+//                                    query c;
+//   O^T (dims x queries) += V^T . P^T   B = P^T straight from the S^T registers (K index
+//                                    order {4g..4g+3, 16+4g..16+4g+3}); A = V^T read by
+//                                    ds_read_b64_tr_b16: within a 16-lane group, lane c reads
+//                                    4 dims of key row 4g + c/4 and receives, after the
+//                                    transpose, keys 4g..4g+3 of dim c.
+// Each lane keeps the online-softmax state of one query.  The causal mask is applied only
+// on the steps that straddle the wave's diagonal or the end of the keys.  The running
+// maximum moves only when a step's maximum exceeds it by more than kRescaleLog2 (log2
+// units), so the accumulators are rescaled rarely and unnormalised weights stay below
+// 2^kRescaleLog2 (well inside bf16 and fp32 range).
 constexpr int kQBlock = 64;
-constexpr int kKTile = 32;   // keys staged per barrier pair
-constexpr int kKSub = 32;    // keys per product step
+constexpr int kTile = 32;     // keys per LDS stage and per softmax step
+constexpr int kStages = 3;    // LDS ring depth: loads run kStages - 1 tiles ahead
 constexpr float kLog2eP = 1.4426950408889634f;
-constexpr float kEmptyP = -1.0e30f;
+constexpr float kRescaleLog2 = 8.0f;
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
 
 struct PrefillParams {
     int B, Hq, Hkv, nqb, group;
@@ -119,22 +128,62 @@ struct PrefillParams {
 
 Q3T_DEVICE bf16x8_t as_bf16x8(const U4 &v) { return __builtin_bit_cast(bf16x8_t, v); }
 
-template <int D, int G>
-__global__ void __launch_bounds__(256) prefill_attention_kernel(PrefillParams p) {
-    // G: query heads per workgroup (a divisor of the GQA group p.group)
-    constexpr int KK = D / 32;   // MFMA steps over the head dimension
-    constexpr int DB = D / 16;   // 16-row blocks of O^T
-    constexpr int KROW = D + 8;  // padded LDS row of K (bf16)
-    constexpr int VROW = kKTile + 2;  // 4-byte rows: the transposed writes of 16 lanes spread over 8 banks
-    constexpr int CPR = D / 8;   // 16-byte chunks per row
-    __shared__ uint16_t sK[kKTile][KROW];
-    __shared__ uint16_t sVt[D][VROW];
+// 8 bytes of LDS per lane, transposed across each 16-lane group as 16-bit elements.
+Q3T_DEVICE uint2 lds_read_tr16(uint32_t byte_addr) {
+    const s16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4_t *)(uintptr_t)byte_addr);
+    return __builtin_bit_cast(uint2, r);
+}
+Q3T_DEVICE U4 lds_read16(uint32_t byte_addr) {
+    const i32x4_t v = *(__attribute__((address_space(3))) const i32x4_t *)(uintptr_t)byte_addr;
+    return __builtin_bit_cast(U4, v);
+}
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// A buffer resource in scalar registers (for inline assembly): base, 32-bit range, raw dwords.
+Q3T_DEVICE i32x4_t scalar_rsrc(const void *base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    i32x4_t r;
+    r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    r.y = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu));
+    r.z = __builtin_amdgcn_readfirstlane((int)bytes);
+    r.w = 0x00020000;
+    return r;
+}
+// 16 bytes per lane from global memory straight into LDS at lds_base + 16 * lane (the wave's
+// lanes fill one contiguous 1 KiB run); offsets past the resource's range write zeros.  The
+// load is issued from inline assembly so that the compiler does not insert a wait for it in
+// front of unrelated LDS reads; completion is awaited explicitly with wait_loads.
+Q3T_DEVICE void load_to_lds16(i32x4_t rsrc, uint32_t voffset, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :: "s"(lds_base), "v"(voffset), "s"(rsrc) : "memory", "m0");
+}
+template <int N>
+Q3T_DEVICE void wait_loads() { asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory"); }
+// Workgroup barrier after the wave's own LDS reads have returned.
+Q3T_DEVICE void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int D, int GH>
+__global__ void __launch_bounds__(256 * GH) __attribute__((amdgpu_waves_per_eu(4)))
+prefill_attention_kernel(PrefillParams p) {
+    constexpr int NT = 256 * GH;                  // threads
+    constexpr int KK = D / 32;                    // MFMA steps over the head dimension
+    constexpr int DB = D / 16;                    // 16-row blocks of O^T
+    constexpr int CPR = D / 8;                    // 16-byte chunks per row
+    constexpr int ROW = D * 2;                    // bytes per row
+    constexpr int KBYTES = kTile * ROW;           // K part of a stage
+    constexpr int SBYTES = 2 * KBYTES;            // stage: K rows, then V rows
+    constexpr int LPT = 2 * kTile * CPR / NT;     // 16-byte loads per thread per tile
+    static_assert(LPT >= 1 && (2 * kTile * CPR) % NT == 0, "a tile is whole loads per thread");
+    static_assert(KBYTES % 1024 == 0, "a wave's load never straddles K and V");
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[kStages * SBYTES];
+
+    // the wave index through readfirstlane: wave-uniform for the compiler too, so that the
+    // per-wave load resources stay in scalar registers
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, c = lane & 15;
-    const int hgroups = p.Hq / G;
-    const int hq0 = (blockIdx.x % hgroups) * G;  // first query head of this workgroup
-    const int h = hq0 / p.group;                  // its KV head
+    const int hgroups = p.Hq / GH;
+    const int hq = (blockIdx.x % hgroups) * GH + wave / 4;  // this wave's query head
+    const int h = hq / p.group;                              // the workgroup's KV head
     const int rest = blockIdx.x / hgroups;
     const int b = rest % p.B;
     const int qb = p.nqb - 1 - rest / p.B;  // the longest blocks are dispatched first
@@ -145,159 +194,171 @@ __global__ void __launch_bounds__(256) prefill_attention_kernel(PrefillParams p)
     if (q0 >= n) return;
     // keys 0 ... kv_end-1 are visible to this block; the arena holds at most `cap` of them
     const int kv_end = (int)min((int64_t)min(n, q0 + kQBlock), p.cap);
-    const int ntiles = (kv_end + kKTile - 1) / kKTile;
+    const int ntiles = (kv_end + kTile - 1) / kTile;
     const int64_t slot = p.slots ? p.slots[b] : b;
-
-    // the wave's query rows as B operands: Q[query c][8g + 32kk ...], zeros past the request
-    const int qpos = q0 + 16 * wave + c;
+    const int wq0 = q0 + 16 * (wave & 3);        // first query of this wave
+    const int wave_end = min(wq0 + 16, kv_end);  // keys [0, wave_end) can be visible to the wave
+    const int mask_from = min(wq0 + 1, kv_end);  // steps reaching past this key need the mask
+    const int qpos = wq0 + c;
     const bool qvalid = qpos < n;
-    bf16x8_t qB[G][KK];
-#pragma unroll
-    for (int j = 0; j < G; ++j) {
-        const char *row = p.q + ((int64_t)(t0 + (qvalid ? qpos : 0)) * p.q_st + (hq0 + j) * p.q_sh) * 2;
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-            U4 v = load16(row + (32 * kk + 8 * g) * 2);
-            if (!qvalid) v = U4{0u, 0u, 0u, 0u};
-            qB[j][kk] = as_bf16x8(v);
-        }
-    }
+    const int lim = min(qpos, kv_end - 1);       // last key visible to this lane's query
 
-    // K/V tile loader: 256 threads x 16 bytes per pass; rows past kv_end read zeros
+    // tile loader: load i of a thread fills LDS slot s = i * NT + tid (16 bytes) of a stage:
+    // row s / CPR (K rows first, then V rows), physical chunk s % CPR, holding logical chunk
+    // (physical ^ swizzle(row)) of key tile * kTile + row
     const char *kbase = p.k + (slot * p.k_sb + h * p.k_sh) * 2;
     const char *vbase = p.v + (slot * p.v_sb + h * p.v_sh) * 2;
-    const auto krs = buffer_rsrc(uniform_ptr(kbase), (uint32_t)((kv_end - 1) * p.k_st * 2 + D * 2));
-    const auto vrs = buffer_rsrc(uniform_ptr(vbase), (uint32_t)((kv_end - 1) * p.v_st * 2 + D * 2));
-    constexpr int PASSES = kKTile * CPR / 256;
-    U4 kreg[PASSES], vreg[PASSES];
-    auto fetch = [&](int kt) {
+    const uint32_t kst = (uint32_t)(p.k_st * 2), vst = (uint32_t)(p.v_st * 2);
+    const i32x4_t krs = scalar_rsrc(kbase, (uint32_t)((kv_end - 1) * kst + D * 2));
+    const i32x4_t vrs = scalar_rsrc(vbase, (uint32_t)((kv_end - 1) * vst + D * 2));
+    const uint32_t ring_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)ring;
+    uint32_t row_off[LPT];
+    int row_of[LPT];
 #pragma unroll
-        for (int ps = 0; ps < PASSES; ++ps) {
-            const int idx = ps * 256 + tid, row = idx / CPR, ch = idx % CPR;
-            const int key = kt * kKTile + row;
-            const bool ok = key < kv_end;
-            kreg[ps] = buffer_load16(krs, ok ? (uint32_t)(key * p.k_st * 2 + ch * 16) : 0xfffffff0u);
-            vreg[ps] = buffer_load16(vrs, ok ? (uint32_t)(key * p.v_st * 2 + ch * 16) : 0xfffffff0u);
-        }
-    };
-    auto stage = [&]() {
+    for (int i = 0; i < LPT; ++i) {
+        const int s = i * NT + tid, rall = s / CPR, pc = s % CPR;
+        const bool is_v = rall >= kTile;
+        const int r = rall % kTile;
+        const int ch = pc ^ ((is_v ? 2 * r : r) & (CPR - 1));
+        row_of[i] = r;
+        row_off[i] = (uint32_t)r * (is_v ? vst : kst) + ch * 16;
+    }
+    auto issue = [&](int kt, int stage) {
 #pragma unroll
-        for (int ps = 0; ps < PASSES; ++ps) {
-            const int idx = ps * 256 + tid, row = idx / CPR, ch = idx % CPR;
-            *reinterpret_cast<U4 *>(&sK[row][ch * 8]) = kreg[ps];
-            const uint32_t w[4] = {vreg[ps].x, vreg[ps].y, vreg[ps].z, vreg[ps].w};
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                sVt[ch * 8 + 2 * m][row] = (uint16_t)(w[m] & 0xffffu);
-                sVt[ch * 8 + 2 * m + 1][row] = (uint16_t)(w[m] >> 16);
-            }
+        for (int i = 0; i < LPT; ++i) {
+            const int first_slot = i * NT + wave * 64;             // wave-uniform
+            const bool is_v = first_slot / CPR >= kTile;
+            const int key0 = kt * kTile;
+            const uint32_t off = row_of[i] < kv_end - key0
+                                     ? row_off[i] + (uint32_t)key0 * (is_v ? vst : kst)
+                                     : 0xfffffff0u;
+            load_to_lds16(is_v ? vrs : krs, off,
+                          (uint32_t)__builtin_amdgcn_readfirstlane((int)(ring_base + stage * SBYTES + first_slot * 16)));
         }
     };
 
-    f32x4_t acc[G][DB];
-    float m[G], l[G];
+    // per-lane LDS read addresses within a stage
+    uint32_t ka[KK], va[DB];
 #pragma unroll
-    for (int j = 0; j < G; ++j) {
-        m[j] = kEmptyP;
-        l[j] = 0.f;
+    for (int kk = 0; kk < KK; ++kk) ka[kk] = c * ROW + (((4 * kk + g) ^ (c & (CPR - 1))) * 16);
+    {
+        const int r = 4 * g + (c >> 2);  // key row of this lane's transposed read (+16 for keys 16..31)
+        const int sw = (2 * r) & (CPR - 1);
 #pragma unroll
-        for (int db = 0; db < DB; ++db) acc[j][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int db = 0; db < DB; ++db)
+            va[db] = KBYTES + r * ROW + (((2 * db + ((c >> 1) & 1)) ^ sw) * 16) + 8 * (c & 1);
     }
 
-    fetch(0);
-    for (int kt = 0; kt < ntiles; ++kt) {
-        __syncthreads();  // every wave is done reading the previous tile
-        stage();
-        __syncthreads();
-        if (kt + 1 < ntiles) fetch(kt + 1);  // in flight during this tile's products
+    // the first tiles go out before anything else waits on memory
 #pragma unroll
-        for (int sub = 0; sub < kKTile / kKSub; ++sub) {
-        const int kbase_idx = kt * kKTile + sub * kKSub;
-        if (kbase_idx > q0 + 16 * wave + 15) break;  // the rest of the tile is above this wave's diagonal
+    for (int s = 0; s < kStages - 1; ++s)
+        if (s < ntiles) issue(s, s);
 
-        // S^T for the 16-key blocks of the tile and every head
-        constexpr int NKB = kKSub / 16;
-        f32x4_t st[NKB][G];
+    // the wave's query rows as B operands: Q[query c][8g + 32kk ...], zeros past the request
+    bf16x8_t qB[KK];
+    {
+        const char *row = p.q + ((int64_t)(t0 + (qvalid ? qpos : 0)) * p.q_st + hq * p.q_sh) * 2;
+        U4 qv[KK];
 #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) {
+        for (int kk = 0; kk < KK; ++kk) qv[kk] = load16(row + (32 * kk + 8 * g) * 2);
 #pragma unroll
-            for (int j = 0; j < G; ++j) st[kb][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int kk = 0; kk < KK; ++kk) {
+            if (!qvalid) qv[kk] = U4{0u, 0u, 0u, 0u};
+            qB[kk] = as_bf16x8(qv[kk]);
+        }
+    }
+
+    f32x4_t acc[DB];
 #pragma unroll
-            for (int kk = 0; kk < KK; ++kk) {
-                const bf16x8_t a = as_bf16x8(*reinterpret_cast<const U4 *>(&sK[sub * kKSub + 16 * kb + c][32 * kk + 8 * g]));
+    for (int db = 0; db < DB; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float m = 0.f, l = 0.f;  // running maximum (scaled log2 units) and this lane's weight sum
+    bool first = true;
+    const float sl = p.scale_log2;
+
+    auto step = [&](int kt, uint32_t sbase) {
+        const int kb0 = kt * kTile;  // first key of the step
+        if (kb0 >= wave_end) return;  // past this wave's keys
+        // S^T for keys kb0 + 16kb + (4g..4g+3)
+        f32x4_t st0 = {0.f, 0.f, 0.f, 0.f}, st1 = {0.f, 0.f, 0.f, 0.f};
+        __builtin_amdgcn_s_setprio(1);  // a wave issuing products goes first, others do the softmax
 #pragma unroll
-                for (int j = 0; j < G; ++j)
-                    st[kb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qB[j][kk], st[kb][j], 0, 0, 0);
+        for (int kk = 0; kk < KK; ++kk) {
+            const bf16x8_t a0 = as_bf16x8(lds_read16(sbase + ka[kk]));
+            const bf16x8_t a1 = as_bf16x8(lds_read16(sbase + ka[kk] + 16 * ROW));
+            st0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qB[kk], st0, 0, 0, 0);
+            st1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qB[kk], st1, 0, 0, 0);
+        }
+        __builtin_amdgcn_s_setprio(0);
+        float x[8] = {st0[0], st0[1], st0[2], st0[3], st1[0], st1[1], st1[2], st1[3]};
+        if (kb0 + kTile > mask_from) {  // the step reaches past the diagonal or the keys
+            const int rel = lim - kb0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (4 * g + i > rel) x[i] = -INFINITY;
+                if (16 + 4 * g + i > rel) x[4 + i] = -INFINITY;
             }
         }
-        // scale, causal mask, online softmax per (head, query c); P^T packed to bf16, one
-        // B operand per 32 keys (blocks 2s and 2s+1)
-        bf16x8_t pB[NKB / 2][G];
+        float mx = x[0];
 #pragma unroll
-        for (int j = 0; j < G; ++j) {
-            float x[NKB * 4];
-            float mx = kEmptyP;
+        for (int e = 1; e < 8; ++e) mx = __builtin_amdgcn_fmed3f(mx, x[e], __builtin_inff());
+        mx = __builtin_amdgcn_fmed3f(mx, xor16(mx), __builtin_inff());
+        mx = __builtin_amdgcn_fmed3f(mx, xor32(mx), __builtin_inff());
+        const float mt = mx * sl;
+        if (first) {
+            m = mt;
+            first = false;
+        } else if (__builtin_amdgcn_ballot_w64(mt > m + kRescaleLog2) != 0) {
+            const float mn = fmaxf(m, mt);
+            const float alpha = fexp2(m - mn);
+            m = mn;
+            l *= alpha;
 #pragma unroll
-            for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int key = kbase_idx + 16 * kb + 4 * g + i;
-                    const float s = st[kb][j][i] * p.scale_log2;
-                    x[kb * 4 + i] = (key <= qpos && key < kv_end) ? s : -INFINITY;
-                    mx = fmaxf(mx, x[kb * 4 + i]);
-                }
-            mx = fmaxf(mx, xor16(mx));
-            mx = fmaxf(mx, xor32(mx));
-            const float mn = fmaxf(m[j], mx);
-            const float alpha = fexp2(m[j] - mn);
-            m[j] = mn;
-            float ps = 0.f;
-            float pv[NKB * 4];
-#pragma unroll
-            for (int e = 0; e < NKB * 4; ++e) {
-                pv[e] = fexp2(x[e] - mn);
-                ps += pv[e];
-            }
-            l[j] = l[j] * alpha + ps;  // this lane's keys only; summed over g at the end
-#pragma unroll
-            for (int db = 0; db < DB; ++db) acc[j][db] *= alpha;
-#pragma unroll
-            for (int sp = 0; sp < NKB / 2; ++sp) {
-                const float *q8 = pv + 8 * sp;
-                const U4 packed = {cvt_pk_bf16(q8[0], q8[1]), cvt_pk_bf16(q8[2], q8[3]),
-                                   cvt_pk_bf16(q8[4], q8[5]), cvt_pk_bf16(q8[6], q8[7])};
-                pB[sp][j] = as_bf16x8(packed);
-            }
+            for (int db = 0; db < DB; ++db) acc[db] *= alpha;
         }
-        // O^T += V^T . P^T, 32 keys per product
+        float pv[8];
 #pragma unroll
-        for (int sp = 0; sp < NKB / 2; ++sp) {
+        for (int e = 0; e < 8; ++e) pv[e] = fexp2(__builtin_fmaf(x[e], sl, -m));
+        l += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+        const U4 packed = {cvt_pk_bf16(pv[0], pv[1]), cvt_pk_bf16(pv[2], pv[3]),
+                           cvt_pk_bf16(pv[4], pv[5]), cvt_pk_bf16(pv[6], pv[7])};
+        const bf16x8_t pB = as_bf16x8(packed);
+        // O^T += V^T . P^T
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-            for (int db = 0; db < DB; ++db) {
-                const uint32_t *row = reinterpret_cast<const uint32_t *>(&sVt[16 * db + c][0]);
-                const int k0 = (sub * kKSub + 32 * sp + 4 * g) / 2, k1 = (sub * kKSub + 32 * sp + 16 + 4 * g) / 2;
-                const bf16x8_t a = as_bf16x8(U4{row[k0], row[k0 + 1], row[k1], row[k1 + 1]});
-#pragma unroll
-                for (int j = 0; j < G; ++j)
-                    acc[j][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pB[sp][j], acc[j][db], 0, 0, 0);
-            }
+        for (int db = 0; db < DB; ++db) {
+            const uint2 lo = lds_read_tr16(sbase + va[db]), hi = lds_read_tr16(sbase + va[db] + 16 * ROW);
+            const bf16x8_t a = as_bf16x8(U4{lo.x, lo.y, hi.x, hi.y});
+            acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pB, acc[db], 0, 0, 0);
         }
-        }
+        __builtin_amdgcn_s_setprio(0);
+    };
+    // one ring position: wait for this tile's loads (later tiles stay in flight), barrier
+    // (every wave is done with the stage the next load overwrites), issue the tile
+    // kStages - 1 ahead into that stage, then the products
+    auto ring_step = [&](int kt, int stage) {
+        if (kt + 1 < ntiles) wait_loads<LPT>();  // the one younger tile stays in flight
+        else wait_loads<0>();
+        lds_barrier();
+        if (kt + kStages - 1 < ntiles) issue(kt + kStages - 1, (stage + kStages - 1) % kStages);
+        step(kt, ring_base + stage * SBYTES);
+    };
+    static_assert(kStages == 3, "the waits above and the unrolled ring below assume three stages");
+    for (int kt = 0; kt < ntiles; kt += kStages) {
+        ring_step(kt, 0);
+        if (kt + 1 < ntiles) ring_step(kt + 1, 1);
+        if (kt + 2 < ntiles) ring_step(kt + 2, 2);
     }
 
     if (!qvalid) return;
+    float lt = l + xor16(l);
+    lt += xor32(lt);
+    const float inv = __builtin_amdgcn_rcpf(lt);
+    char *orow = p.out + ((int64_t)(t0 + qpos) * p.o_st + hq * p.o_sh) * 2;
 #pragma unroll
-    for (int j = 0; j < G; ++j) {
-        float lt = l[j] + xor16(l[j]);
-        lt += xor32(lt);
-        const float inv = __builtin_amdgcn_rcpf(lt);
-        char *orow = p.out + ((int64_t)(t0 + qpos) * p.o_st + (hq0 + j) * p.o_sh) * 2;
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-            const uint2 v = {cvt_pk_bf16_canon(acc[j][db][0] * inv, acc[j][db][1] * inv),
-                             cvt_pk_bf16_canon(acc[j][db][2] * inv, acc[j][db][3] * inv)};
-            *reinterpret_cast<uint2 *>(orow + (16 * db + 4 * g) * 2) = v;
-        }
+    for (int db = 0; db < DB; ++db) {
+        const uint2 v = {cvt_pk_bf16(acc[db][0] * inv, acc[db][1] * inv),
+                         cvt_pk_bf16(acc[db][2] * inv, acc[db][3] * inv)};
+        *reinterpret_cast<uint2 *>(orow + (16 * db + 4 * g) * 2) = v;
     }
 }
 
@@ -343,9 +404,10 @@ extern "C" int q3t_prefill_rope_write(const q3t_prefill_rope_write_args *a, void
 }
 
 
-template <int D, int G>
+template <int D, int GH>
 static void launch_prefill(const PrefillParams &p, hipStream_t s) {
-    hipLaunchKernelGGL((prefill_attention_kernel<D, G>), dim3((uint32_t)p.B * p.nqb * (p.Hq / G)), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((prefill_attention_kernel<D, GH>), dim3((uint32_t)p.B * p.nqb * (p.Hq / GH)),
+                       dim3(256 * GH), 0, s, p);
 }
 
 extern "C" int q3t_prefill_attention(const q3t_prefill_args *a, void *stream) {
@@ -384,9 +446,13 @@ extern "C" int q3t_prefill_attention(const q3t_prefill_args *a, void *stream) {
     p.T = a->total_tokens;
     p.out = (char *)a->out; p.o_st = a->o_stride_t; p.o_sh = a->o_stride_h;
     hipStream_t s = (hipStream_t)stream;
-    // one query head per workgroup: the accumulators of a single head keep the kernel at a
-    // register count that leaves two workgroups per CU's SIMDs busy
-    if (a->head_dim == 128) launch_prefill<128, 1>(p, s);
-    else launch_prefill<64, 1>(p, s);
+    // the query heads of a KV head pair up in one workgroup and share its staged K/V tiles
+    if (G % 2 == 0) {
+        if (a->head_dim == 128) launch_prefill<128, 2>(p, s);
+        else launch_prefill<64, 2>(p, s);
+    } else {
+        if (a->head_dim == 128) launch_prefill<128, 1>(p, s);
+        else launch_prefill<64, 1>(p, s);
+    }
     return launch_status();
 }
