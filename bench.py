@@ -202,6 +202,29 @@ def cpu_baseline(seconds: float, threads: int = 0):
                        f"cores in the affinity mask) = {layer_s * 1e3:.2f} ms, scaled to a 28-layer step")}
 
 
+def arena_move_detail(pkg, arena, contexts, reps=20):
+    """One compaction move on the talker arena (all 56 planes, capacity 1024): the whole slot
+    row, as the reference copies it, against the moved request's prefix [:position + 1]
+    (SlotArena.move(length=...)).  Moves the last slot into slot 0 (after all timing)."""
+    last = arena.shape[1] - 1
+    length = int(contexts[last]) + 1
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    out = {}
+    for name, n in (("full_row", arena.shape[3]), ("prefix", length)):
+        dst, src = arena[:, 0, :, :n], arena[:, last, :, :n]
+        pkg.copy_rows(dst, src)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(reps):
+            pkg.copy_rows(dst, src)
+        stop.record()
+        torch.cuda.synchronize()
+        us = start.elapsed_time(stop) * 1e3 / reps
+        nbytes = 2 * dst.numel() * dst.element_size()  # read + write
+        out[name] = {"rows": n, "us": us, "bytes": nbytes, "GBs": nbytes / (us * 1e-6) / 1e9}
+    return out
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -306,6 +329,7 @@ def main():
 
     prefill = prefill_detail(pkg, device)
     predictor = predictor_detail(pkg, device)
+    moves = arena_move_detail(pkg, arena, contexts)
     traffic = read_traffic()
     result = {
         "metric": "decode-attn tokens/s + achieved HBM GB/s, 64-req ragged talker step, 1 GPU",
@@ -336,7 +360,8 @@ def main():
                    "max_chunks": args.max_chunks,
                    "wall_s_timed_region": wall,
                    "prefill": prefill,
-                   "predictor": predictor},
+                   "predictor": predictor,
+                   "arena_move": moves},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

@@ -19,6 +19,11 @@ Mirrors the bookkeeping of the reference's ``ContinuousModel`` (qwen3_tts_engine
 Only the integer state lives here; with an arena attached, the moves, loads and regrowths
 run as the package's HIP copy kernels, in the order the reference issues them.  Every
 operation is also recorded in ``ops`` for inspection.
+
+``compact_prefix=True`` keeps the integer state identical but shrinks the copies to what can
+still be read: a compaction move copies the moved request's rows ``[:position + 1]`` instead
+of the whole capacity, and a regrowth copies only the slots in use.  Rows past a request's
+position are always written before they are read, so every attended row is unchanged.
 """
 from __future__ import annotations
 
@@ -67,7 +72,8 @@ def grown_capacity(capacity: int, required: int) -> int:
 class SlotScheduler:
     """Dense slot table of a continuous batch (one model-owner thread drives it)."""
 
-    def __init__(self, max_slots, capacity=512, decode_bucket_step=0, bucket_kv=False, arena=None):
+    def __init__(self, max_slots, capacity=512, decode_bucket_step=0, bucket_kv=False, arena=None,
+                 compact_prefix=False):
         if max_slots < 1 or max_slots & (max_slots - 1):
             raise ValueError('Continuous slot count must be a positive power of two')
         decode_batch_size(1, max_slots, decode_bucket_step)  # validates the bucket step
@@ -75,6 +81,7 @@ class SlotScheduler:
         self.decode_bucket_step = decode_bucket_step
         self.bucket_kv = bucket_kv
         self.arena = arena
+        self.compact_prefix = compact_prefix
         self.capacity = arena.capacity if arena is not None else capacity
         self.states: list[SlotState] = []
         self.ops: list[tuple] = []
@@ -86,7 +93,8 @@ class SlotScheduler:
             return
         self.ops.append(('grow', self.capacity, new))
         if self.arena is not None:
-            self.arena = grow_arena(self.arena, required)
+            active = len(self.states) if self.compact_prefix else None
+            self.arena = grow_arena(self.arena, required, active=active)
         self.capacity = new
 
     def _retire(self, index: int) -> None:
@@ -94,7 +102,8 @@ class SlotScheduler:
         if last != index:
             self.ops.append(('move', last, index))
             if self.arena is not None:
-                self.arena.move(last, index)
+                length = self.states[last].position + 1 if self.compact_prefix else None
+                self.arena.move(last, index, length=length)
             self.states[index] = self.states[last]
         self.states.pop()
 

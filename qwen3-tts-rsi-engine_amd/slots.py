@@ -49,9 +49,26 @@ class SlotArena:
             copy_rows(self.keys[i][slot, :, :length], layer.keys[row, :, :length])
             copy_rows(self.values[i][slot, :, :length], layer.values[row, :, :length])
 
-    def move(self, source, destination):
-        """Compaction: the whole slot row ``source`` overwrites ``destination`` in every layer."""
+    def move(self, source, destination, length=None):
+        """Compaction: slot row ``source`` overwrites ``destination`` in every layer.
+
+        ``length=None`` copies the whole row, as the reference does (continuous.py:124-128).
+        With ``length``, only positions ``[:length]`` are copied: a request at position p
+        reads rows ``[0, p]`` and writes row p before reading it, so rows past its position
+        are never read before they are written, and the copy shrinks from the capacity to
+        the request's own length."""
         if source == destination:
+            return
+        if length is not None:
+            length = min(int(length), self.capacity)
+            if length <= 0:
+                return
+            if self.packed is not None:
+                copy_rows(self.packed[:, destination, :, :length], self.packed[:, source, :, :length])
+                return
+            for keys, values in zip(self.keys, self.values):
+                copy_rows(keys[destination, :, :length], keys[source, :, :length])
+                copy_rows(values[destination, :, :length], values[source, :, :length])
             return
         if self.packed is not None:
             copy_rows(self.packed[:, destination], self.packed[:, source])
@@ -68,19 +85,25 @@ class SlotArena:
         return self.keys + self.values
 
 
-def grow_arena(old: SlotArena, required: int) -> SlotArena:
+def grow_arena(old: SlotArena, required: int, active: int | None = None) -> SlotArena:
     """A larger arena holding ``old``'s contents, with the reference's capacity rule
-    max(2*C, 2**bit_length(required)) (continuous.py:353-363).  ``required < C`` returns ``old``."""
+    max(2*C, 2**bit_length(required)) (continuous.py:353-363).  ``required < C`` returns ``old``.
+
+    ``active=None`` copies every slot, as the reference does; ``active=n`` copies only slots
+    ``[0, n)`` (the dense slots in use: a free slot is loaded from a prefill before it is read)."""
     if required < old.capacity:
         return old
     capacity = max(old.capacity * 2, 1 << int(required).bit_length())
     new = SlotArena(old.reference, old.slots, capacity, old.native_kv_update, old.triton_kv_update,
                     packed_kv=old.packed_kv)
+    used = old.slots if active is None else max(0, min(int(active), old.slots))
+    if used == 0:
+        return new
     if new.packed is not None:
-        copy_rows(new.packed[:, :, :, :old.capacity], old.packed)
+        copy_rows(new.packed[:, :used, :, :old.capacity], old.packed[:, :used])
     else:
         for target, source in zip(new.planes(), old.planes()):
-            copy_rows(target[:, :, :old.capacity], source)
+            copy_rows(target[:used, :, :old.capacity], source[:used])
     return new
 
 

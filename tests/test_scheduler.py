@@ -67,7 +67,12 @@ def test_scheduler_rejects_invalid_geometry(pkg):
 
 
 @pytest.mark.gpu
-def test_arena_follows_the_scheduler_bit_exact(pkg, device):
+@pytest.mark.parametrize("compact_prefix", [False, True])
+def test_arena_follows_the_scheduler_bit_exact(pkg, device, compact_prefix):
+    """The arena driven by the scheduler equals a numpy mirror of the reference's operations
+    (full-row moves and regrowth copies).  With ``compact_prefix`` the moves copy only
+    ``[:position + 1]`` and regrowth only the slots in use, so the comparison covers the rows
+    every active request can still read: ``[:position]`` of each slot in use."""
     from qwen3_tts_engine_amd.scheduler import SlotScheduler
     from qwen3_tts_engine_amd.slots import SlotArena
 
@@ -83,12 +88,14 @@ def test_arena_follows_the_scheduler_bit_exact(pkg, device):
 
     layers, slots, heads, width = 2, 8, 2, 16
     arena = SlotArena(Talker().to(device), slots, 16, packed_kv=True)
-    sched = SlotScheduler(slots, 16, decode_bucket_step=4, bucket_kv=True, arena=arena)
+    sched = SlotScheduler(slots, 16, decode_bucket_step=4, bucket_kv=True, arena=arena,
+                          compact_prefix=compact_prefix)
     mirror = np.zeros((2 * layers, slots, heads, 16, width), dtype=np.uint16)
     trace = osched.make_trace(seed=5, iterations=60, mean_arrivals=0.6, prompt=(3, 20), lengths=(4, 30),
                               cancel_rate=0.1)
     gen = torch.Generator().manual_seed(6)
     queue, active = [], []
+    moves = 0
     for it, batch in enumerate(trace['arrivals']):
         queue.extend(batch)
         cancelled = [active[0]] if active and trace['cancels'][it] < trace['cancel_rate'] else []
@@ -103,6 +110,7 @@ def test_arena_follows_the_scheduler_bit_exact(pkg, device):
         sched.cancel(cancelled)
         sched.admit(subs, prefill.to(device) if prefill is not None else None)
         record = sched.decode_batch()
+        moves += sum(op[0] == 'move' for op in sched.ops)
         # mirror the recorded operations on numpy
         for op in sched.ops:
             if op[0] == 'grow':
@@ -127,10 +135,56 @@ def test_arena_follows_the_scheduler_bit_exact(pkg, device):
             for op in sched.ops:
                 assert op[0] == 'move'
                 mirror[:, op[2]] = mirror[:, op[1]]
+                moves += 1
         else:
             done = []
         torch.cuda.synchronize()
-        assert np.array_equal(bits(sched.arena.packed), mirror), f"iteration {it}"
+        if compact_prefix:
+            got = bits(sched.arena.packed)
+            for slot, state in enumerate(sched.states):
+                n = state.position
+                assert np.array_equal(got[:, slot, :, :n], mirror[:, slot, :, :n]), f"iteration {it} slot {slot}"
+        else:
+            assert np.array_equal(bits(sched.arena.packed), mirror), f"iteration {it}"
         active = [i for i in active if i not in cancelled and i not in done]
         active.extend(i for i, _, _ in subs if i not in done)
-    assert sched.capacity > 16
+    assert sched.capacity > 16 and moves > 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("packed", [True, False])
+def test_prefix_move_and_active_regrowth(pkg, device, packed):
+    """move(length=n) copies rows [:n] of every plane and leaves the destination's tail and
+    every other slot untouched; grow_arena(active=n) carries slots [0, n) over unchanged."""
+    from qwen3_tts_engine_amd.slots import SlotArena, grow_arena
+
+    class Config:
+        num_key_value_heads, head_dim, num_hidden_layers = 2, 16, 3
+
+    class Talker(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.config = Config()
+            self.layers = torch.nn.ModuleList([torch.nn.Identity() for _ in range(3)])
+            self.weight = torch.nn.Parameter(torch.zeros(1, dtype=torch.bfloat16))
+
+    arena = SlotArena(Talker().to(device), 6, 24, packed_kv=packed)
+    gen = torch.Generator().manual_seed(9)
+    for plane in arena.planes():
+        plane.copy_(torch.randn(plane.shape, generator=gen).bfloat16().to(device))
+    before = [bits(plane).copy() for plane in arena.planes()]
+    arena.move(4, 1, length=7)
+    torch.cuda.synchronize()
+    for plane, old in zip(arena.planes(), before):
+        expected = old.copy()
+        expected[1, :, :7] = old[4, :, :7]
+        assert np.array_equal(bits(plane), expected)
+    arena.move(2, 0, length=100)  # clipped to the capacity: the whole row
+    torch.cuda.synchronize()
+    snapshot = [bits(plane).copy() for plane in arena.planes()]
+    assert all(np.array_equal(p[0], p[2]) for p in snapshot)
+    grown = grow_arena(arena, 30, active=3)
+    torch.cuda.synchronize()
+    assert grown.capacity == 48
+    for plane, old in zip(grown.planes(), snapshot):
+        assert np.array_equal(bits(plane)[:3, :, :24], old[:3])
