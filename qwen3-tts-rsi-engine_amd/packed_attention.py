@@ -15,6 +15,10 @@ signature compatibility):
   and k, the paired K/V write at the cache positions and ragged GQA attention over keys
   0 ... position (the ``j <= pos[b]`` mask of SlotGraph.compute, continuous.py:191-192,
   which the reference adds as 0 / finfo.min);
+* so is an unmasked one-token step s >= 1 of the code predictor over a ``PredictorCache``:
+  it writes position s + 1 and attends positions 0 ... s + 1 (predictor.py:19-24, the
+  unmasked steps of UniformPredictor.run, continuous.py:55-62), which is ``decode_step`` with
+  every position at s + 1;
 * every other call rotates q/k with ``rotary`` (bf16-exact to torch eager), lets the cache
   update and calls ``attention`` (the npu_attention.attention drop-in).
 """
@@ -24,7 +28,7 @@ import torch
 
 from .attention import attention, decode_step
 from .rotary import rotary
-from .slots import SlotCache
+from .slots import PredictorCache, SlotCache
 
 _ATTENTION_CLASSES = ('Qwen3TTSTalkerAttention', 'Qwen3TTSAttention')
 
@@ -87,6 +91,24 @@ class PackedAttention(torch.nn.Module):
         sin = sin.expand(batch, length, sin.shape[-1]).contiguous()
         return cos, sin
 
+    def _fused_target(self, cache, attention_mask, batch, length, query):
+        """(keys, values, positions) of a one-token step the fused launch can take, else None."""
+        reference = self.reference
+        if (length != 1 or reference.training or query.dtype != torch.bfloat16
+                or reference.head_dim != 128):
+            return None
+        layer = reference.layer_idx
+        if isinstance(cache, SlotCache):
+            keys, values = cache.arena.keys[layer], cache.arena.values[layer]
+            if keys.is_contiguous() and values.is_contiguous():
+                return keys, values, cache.positions
+        elif isinstance(cache, PredictorCache) and cache.step >= 1 and attention_mask is None:
+            keys, values = cache.keys[layer], cache.values[layer]
+            if (keys.is_contiguous() and values.is_contiguous() and keys.shape[0] == batch
+                    and cache.step + 1 < keys.shape[2]):
+                return keys, values, cache.positions_at(batch, cache.step + 1, query.device)
+        return None
+
     def forward(self, hidden_states, position_embeddings, attention_mask, past_key_values=None,
                 cache_position=None, **kwargs):
         reference = self.reference
@@ -100,13 +122,11 @@ class PackedAttention(torch.nn.Module):
         value = value.reshape(heads)
         cos, sin = self._tables(position_embeddings, batch, length)
 
-        if (isinstance(past_key_values, SlotCache) and length == 1 and not reference.training
-                and query.dtype == torch.bfloat16 and reference.head_dim == 128
-                and past_key_values.arena.keys[reference.layer_idx].is_contiguous()):
-            arena = past_key_values.arena
-            output = decode_step(query, key, value, arena.keys[reference.layer_idx],
-                                 arena.values[reference.layer_idx], past_key_values.positions,
-                                 cos[:, 0], sin[:, 0], scale=reference.scaling)
+        fused = self._fused_target(past_key_values, attention_mask, batch, length, query)
+        if fused is not None:
+            keys, values, positions = fused
+            output = decode_step(query, key, value, keys, values, positions, cos[:, 0], sin[:, 0],
+                                 scale=reference.scaling)
             return reference.o_proj(output.reshape(*shape, -1)), None
 
         query = rotary(query.contiguous(), cos, sin).transpose(1, 2)

@@ -147,9 +147,13 @@ class PredictorCache(Cache):
         self.step = 0
         self._starts = {}
 
-    def _start_positions(self, batch, start, device):
+    def positions_at(self, batch, start, device):
+        """A device tensor of ``batch`` copies of ``start`` (the write position of a step),
+        kept alive for graph replays."""
         key = (batch, start, device)
-        if key not in self._starts:  # constant per (batch, step): kept alive for graph replays
+        if key not in self._starts:
+            if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+                raise RuntimeError('PredictorCache positions must be created by an eager step before capture')
             self._starts[key] = torch.full((batch,), start, device=device, dtype=torch.int64)
         return self._starts[key]
 
@@ -158,7 +162,7 @@ class PredictorCache(Cache):
         end = self.step + 2
         if keys.shape[2] != end - start:
             raise ValueError('predictor step writes one token (two at step 0)')
-        positions = self._start_positions(keys.shape[0], start, keys.device)
+        positions = self.positions_at(keys.shape[0], start, keys.device)
         kv_write.write_tokens(keys, values, self.keys[layer_index], self.values[layer_index], positions)
         return self.keys[layer_index][:, :, :end], self.values[layer_index][:, :, :end]
 

@@ -171,5 +171,36 @@ def test_predictor_first_step_two_queries_with_mask(pkg, device):
     assert_attention_close(out.detach().float().cpu().numpy().reshape(batch, 2, HQ, D), expected)
 
 
+@pytest.mark.parametrize("step", [1, 7, 14])
+def test_predictor_later_step_is_one_fused_launch(pkg, device, step):
+    """Code predictor step s >= 1 (no mask): the new token is written at s + 1 and attends
+    positions 0 ... s + 1 (predictor.py:19-24), taken by the fused launch with every
+    position at s + 1.  Earlier positions hold random rotated keys from previous steps."""
+    batch, hidden_size = 10, 256
+    model = _Model(Qwen3TTSAttention, 2, hidden_size).to(device).eval()
+    pkg.install_packed_attention(model, native_gqa=True)
+    module = model.layers[1].self_attn
+    gen = torch.Generator().manual_seed(20 + step)
+    hidden = torch.randn(batch, 1, hidden_size, generator=gen).bfloat16().to(device)
+    cache = pkg.PredictorCache(model, hidden)
+    for plane in cache.keys + cache.values:
+        plane.copy_(torch.randn(plane.shape, generator=gen).bfloat16().to(device))
+    cache.step = step
+    keys_before, values_before = bits(cache.keys[1]).copy(), bits(cache.values[1]).copy()
+    pos = torch.full((batch, 1), step + 1, device=device, dtype=torch.int64)
+    cos, sin = pkg.rope_tables(pos, D)
+    q, k, v = _projected(module, hidden)
+    out, _ = module(hidden, (cos, sin), None, past_key_values=cache, cache_position=pos[0])
+    torch.cuda.synchronize()
+    cb, sb = bits(cos)[:, :, None, :], bits(sin)[:, :, None, :]
+    q_rot = obf16.from_bits(orope.rope_bf16(bits(q), cb, sb))
+    k_rot = orope.rope_bf16(bits(k), cb, sb).transpose(0, 2, 1, 3)
+    ek, ev = okv.kv_write(keys_before, values_before, k_rot, bits(v).transpose(0, 2, 1, 3),
+                          np.full(batch, step + 1))
+    assert np.array_equal(bits(cache.keys[1]), ek) and np.array_equal(bits(cache.values[1]), ev)
+    expected = oatt.decode_attention(q_rot, obf16.from_bits(ek), obf16.from_bits(ev), [step + 1] * batch, D ** -0.5)
+    assert_attention_close(out.detach().float().cpu().numpy().reshape(batch, 1, HQ, D), expected)
+
+
 def f64v(v):
     return v.detach().float().cpu().numpy().transpose(0, 2, 1, 3).astype(np.float64)
