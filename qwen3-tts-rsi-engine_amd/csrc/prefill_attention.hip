@@ -185,11 +185,47 @@ prefill_attention_kernel(PrefillParams p) {
     const int hq = (blockIdx.x % hgroups) * GH + wave / 4;  // this wave's query head
     const int h = hq / p.group;                              // the workgroup's KV head
     const int rest = blockIdx.x / hgroups;
-    const int b = rest % p.B;
-    const int qb = p.nqb - 1 - rest / p.B;  // the longest blocks are dispatched first
-    const int t0 = p.cu[b];
-    if (t0 < 0 || t0 >= p.T) return;
-    const int n = (int)min((int64_t)(p.cu[b + 1] - t0), p.T - t0);  // rows past the packed tokens do not exist
+    // Work item `rest` of this head group: a (64-query block qb, request b) pair, numbered with
+    // the longest blocks first.  Up to 64 requests the numbering is dense: only pairs with
+    // rows exist, so the grid's round-robin placement over shader engines sees real work
+    // evenly (empty slots in between would pile long blocks onto some engines and stall the
+    // in-order dispatch behind them).  Lane i holds request i's row range; each level counts
+    // the requests with a block there (ballot) and the item's request is picked by rank
+    // (mbcnt), all wave-uniform, with no memory access beyond the row offsets.
+    int b, qb, t0, n;
+    if (p.B <= 64) {
+        int start = 0, rows = 0;
+        if (lane < p.B) {
+            start = p.cu[lane];
+            rows = (start < 0 || start >= p.T) ? 0 : (int)min((int64_t)(p.cu[lane + 1] - start), p.T - start);
+        }
+        const int blocks = rows > 0 ? (rows + kQBlock - 1) / kQBlock : 0;
+        int remaining = rest;
+        qb = -1;
+        b = 0;
+        for (int level = p.nqb - 1; level >= 0; --level) {
+            const uint64_t has = __builtin_amdgcn_ballot_w64(blocks > level);
+            const int count = __builtin_popcountll(has);
+            if (remaining < count) {
+                const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(has >> 32),
+                                                                __builtin_amdgcn_mbcnt_lo((uint32_t)has, 0u));
+                const uint64_t pick = __builtin_amdgcn_ballot_w64(blocks > level && (int)rank == remaining);
+                b = __builtin_ctzll(pick);
+                qb = level;
+                break;
+            }
+            remaining -= count;
+        }
+        if (qb < 0) return;  // past the last block with rows
+        t0 = __builtin_amdgcn_readlane(start, b);
+        n = __builtin_amdgcn_readlane(rows, b);
+    } else {
+        b = rest % p.B;
+        qb = p.nqb - 1 - rest / p.B;  // the longest blocks are dispatched first
+        t0 = p.cu[b];
+        if (t0 < 0 || t0 >= p.T) return;
+        n = (int)min((int64_t)(p.cu[b + 1] - t0), p.T - t0);  // rows past the packed tokens do not exist
+    }
     const int q0 = qb * kQBlock;
     if (q0 >= n) return;
     // keys 0 ... kv_end-1 are visible to this block; the arena holds at most `cap` of them

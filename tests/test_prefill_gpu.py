@@ -85,6 +85,24 @@ def test_prefill_attention_tile_edges(pkg, device, group, head_dim):
     assert_attention_close(f64(out), expected)
 
 
+@pytest.mark.parametrize("batch", [64, 80])
+def test_prefill_many_requests(pkg, device, batch):
+    """64 requests (the most the kernel numbers densely, longest blocks first) and 80 (the
+    plain request-major numbering), with empty and one-token requests among them."""
+    gen = torch.Generator().manual_seed(batch)
+    lengths = torch.randint(0, 140, (batch,), generator=gen).tolist()
+    lengths[3], lengths[10] = 0, 1
+    kv_heads, q_heads, head_dim = 2, 4, 128
+    q, _, _, cu, _ = _packed(lengths, q_heads, kv_heads, head_dim, 30)
+    dg = torch.Generator(device=device).manual_seed(31)
+    ak = torch.randn(batch, kv_heads, 144, head_dim, generator=dg, device=device, dtype=torch.bfloat16)
+    av = torch.randn(batch, kv_heads, 144, head_dim, generator=dg, device=device, dtype=torch.bfloat16)
+    out = torch.full((q.shape[0], q_heads, head_dim), float('nan'), device=device, dtype=torch.bfloat16)
+    pkg.prefill_attention(q.to(device), ak, av, cu.to(device), max(lengths), out=out)
+    expected = oatt.prefill_attention(f64(q), f64(ak), f64(av), cu.numpy(), head_dim ** -0.5)
+    assert_attention_close(f64(out), expected)
+
+
 def test_prefill_keys_past_capacity_do_not_exist(pkg, device):
     """A prompt longer than the arena: queries attend only keys below the capacity."""
     lengths, capacity = [40, 20], 32
