@@ -202,7 +202,7 @@ def cpu_baseline(seconds: float, threads: int = 0):
                        f"cores in the affinity mask) = {layer_s * 1e3:.2f} ms, scaled to a 28-layer step")}
 
 
-def slot_graph_detail(pkg, device, contexts, reps=50):
+def slot_graph_detail(pkg, device, contexts, reps=50, fused_qk_norm=False):
     """The talker decode step as the reference replays it (SlotGraph.run, continuous.py:217-223):
     a stand-in talker with the real attention shapes (hidden 2048, 28 layers, 16/8 heads,
     head_dim 128; input RMSNorm + attention block + residual per layer, no MLP), the drop-in
@@ -211,7 +211,8 @@ def slot_graph_detail(pkg, device, contexts, reps=50):
     from tests._talker import Talker
     batch = len(contexts)
     model = Talker(layers=LAYERS, hidden=2048, q_heads=HQ, kv_heads=HKV, head_dim=D, seed=0).to(device).eval()
-    pkg.install_packed_attention(model, native_gqa=True, text_only_rope=True, triton_talker_rope=True)
+    pkg.install_packed_attention(model, native_gqa=True, text_only_rope=True, triton_talker_rope=True,
+                                 fused_qk_norm=fused_qk_norm)
     arena = pkg.SlotArena(model, batch, CAPACITY, packed_kv=True)
     graph = pkg.SlotGraph(arena, batch)
     graph.capture()
@@ -234,6 +235,7 @@ def slot_graph_detail(pkg, device, contexts, reps=50):
     torch.cuda.empty_cache()
     return {"workload": "SlotGraph.run of a 28-layer talker attention stack (hidden 2048), 64 requests, "
                         "seed-0 positions, arena capacity 1024",
+            "fused_qk_norm": fused_qk_norm,
             "us_per_step": step_us, "us_per_layer": step_us / LAYERS,
             "tokens_per_s": batch / (step_us * 1e-6)}
 
@@ -367,6 +369,7 @@ def main():
     predictor = predictor_detail(pkg, device)
     moves = arena_move_detail(pkg, arena, contexts)
     talker_step = slot_graph_detail(pkg, device, contexts)
+    talker_step_fused_norm = slot_graph_detail(pkg, device, contexts, fused_qk_norm=True)
     traffic = read_traffic()
     result = {
         "metric": "decode-attn tokens/s + achieved HBM GB/s, 64-req ragged talker step, 1 GPU",
@@ -399,7 +402,8 @@ def main():
                    "prefill": prefill,
                    "predictor": predictor,
                    "arena_move": moves,
-                   "talker_attention_step": talker_step},
+                   "talker_attention_step": talker_step,
+                   "talker_attention_step_fused_qk_norm": talker_step_fused_norm},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

@@ -163,6 +163,12 @@ typedef struct q3t_decode_args {
     int64_t workspace_bytes;
     int64_t max_chunks;      /* chunks per request and KV head, <= 1024; <= 0: enough for
                                 about 2048 workgroups over the batch */
+    /* fused only, optional: RMSNorm of the query rows / the new key rows before RoPE (the
+       q_norm / k_norm of the attention module, packed_attention.py:42-45):
+       bf16(weight * bf16(x * rsqrt(mean(x^2) + norm_eps))) with the fp32 sum of squares of a
+       row; weights are bf16 (head_dim,); NULL = that row is used as given */
+    const void *q_norm_weight, *k_norm_weight;
+    float norm_eps;
 } q3t_decode_args;
 
 /* Bytes of workspace needed by q3t_decode_attention for these sizes. */

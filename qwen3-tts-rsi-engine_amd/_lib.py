@@ -46,6 +46,7 @@ class DecodeArgs(ctypes.Structure):
         ("nk_stride_b", c_i64), ("nk_stride_h", c_i64), ("nv_stride_b", c_i64), ("nv_stride_h", c_i64),
         ("cos", c_vp), ("sin", c_vp), ("cs_stride_b", c_i64),
         ("workspace", c_vp), ("workspace_bytes", c_i64), ("max_chunks", c_i64),
+        ("q_norm_weight", c_vp), ("k_norm_weight", c_vp), ("norm_eps", ctypes.c_float),
     ]
 
 

@@ -124,13 +124,19 @@ def decode_attention(query, keys, values, positions, *, scale=None, mask=None, k
 
 
 def decode_step(query, new_key, new_value, key_arena, value_arena, positions, cos, sin, *,
-                scale=None, out=None, max_chunks=0):
+                scale=None, out=None, max_chunks=0, q_norm_weight=None, k_norm_weight=None,
+                norm_eps=1e-6):
     """Fused one-token decode for a layer.
 
     query (B, 1, Hq, D), new_key/new_value (B, 1, Hkv, D): un-rotated bf16 rows (views of the
     fused QKV projection are fine); key_arena/value_arena (slots >= B, Hkv, C, D) contiguous;
     positions (B,) int64; cos/sin (B, D) or (B, 1, D) bf16.  Writes the rotated key and the
-    value at positions[b] and returns the attention output (B, 1, Hq, D)."""
+    value at positions[b] and returns the attention output (B, 1, Hq, D).
+
+    With ``q_norm_weight`` / ``k_norm_weight`` (bf16 (D,)) the query / key rows are first
+    RMS-normalised in the kernel (the module's q_norm / k_norm, eps ``norm_eps``): raw
+    projection rows go in and no separate norm kernels run.  The fp32 row sums follow the
+    kernel's order, so a result can differ from another implementation's in the last bf16 bit."""
     if query.ndim != 4 or query.shape[1] != 1 or new_key.ndim != 4 or new_key.shape[1] != 1:
         raise ValueError('fused decode expects one-token BSND rows')
     batch, _, q_heads, head_dim = query.shape
@@ -177,6 +183,14 @@ def decode_step(query, new_key, new_value, key_arena, value_arena, positions, co
     a.cos, a.sin = cos2.data_ptr(), sin2.data_ptr()
     a.cs_stride_b = cos2.stride(0)
     a.max_chunks = int(max_chunks)
+    for name, weight in (('q_norm_weight', q_norm_weight), ('k_norm_weight', k_norm_weight)):
+        if weight is None:
+            continue
+        if weight.shape != (head_dim,) or weight.dtype != torch.bfloat16 or not weight.is_contiguous():
+            raise ValueError(f'{name} must be a contiguous bf16 ({head_dim},) tensor')
+        _lib.require_gpu(weight)
+        setattr(a, name, weight.data_ptr())
+    a.norm_eps = float(norm_eps)
     _run_decode(a, device, 'fused decode step')
     return out
 

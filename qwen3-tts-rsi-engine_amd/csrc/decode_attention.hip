@@ -58,6 +58,8 @@ struct DecodeParams {
     int64_t cs_sb;
     float *partials;
     int *counters;
+    const char *qnw, *knw;  // fused: optional RMSNorm weights (bf16, D) of query / new key rows
+    float eps;
 };
 
 Q3T_DEVICE int mask_elem_size(int dtype) { return dtype == Q3T_F32 ? 4 : dtype == Q3T_BOOL ? 1 : 2; }
@@ -108,6 +110,32 @@ Q3T_DEVICE float cross_max(float x) {
     if constexpr (LPK <= 8) x = fmaxf(x, xor8(x));
     if constexpr (LPK <= 16) x = fmaxf(x, xor16(x));
     return fmaxf(x, xor32(x));
+}
+
+// RMSNorm of one bf16 row spread over LPK lanes (8 elements per lane), as the attention
+// module's q_norm / k_norm compute it: fp32 sum of squares over the row, x * rsqrt(mean + eps)
+// rounded to bf16, times the bf16 weight, rounded to bf16.  The sum's order is this kernel's
+// (lanes, then the DPP tree); rows agree with other orders to the last bf16 bit except near
+// rounding ties.
+template <int LPK>
+Q3T_DEVICE U4 rms_norm8(const U4 &x, const U4 &w, float eps, int width) {
+    const uint32_t v[4] = {x.x, x.y, x.z, x.w}, g[4] = {w.x, w.y, w.z, w.w};
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float a = bf16_lo(v[i]), b = bf16_hi(v[i]);
+        ss = __builtin_fmaf(a, a, ss);
+        ss = __builtin_fmaf(b, b, ss);
+    }
+    ss = group_sum<LPK>(ss);
+    const float r = __builtin_amdgcn_rsqf(ss * (1.0f / (float)width) + eps);
+    uint32_t y[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t n = cvt_pk_bf16(bf16_lo(v[i]) * r, bf16_hi(v[i]) * r);
+        y[i] = cvt_pk_bf16_canon(bf16_lo(n) * bf16_lo(g[i]), bf16_hi(n) * bf16_hi(g[i]));
+    }
+    return U4{y[0], y[1], y[2], y[3]};
 }
 
 // Cross-workgroup chunk states are written and read with device-scope (sc1) accesses, which
@@ -283,11 +311,19 @@ decode_attention_kernel(DecodeParams p) {
     const auto vrs = buffer_rsrc(uniform_ptr(vb), (uint32_t)((p.ctx - 1) * vst + D * ES));
 
     if constexpr (FUSED) {
+        if (p.qnw) {
+            const U4 w = load16(p.qnw + cl * 16);
+#pragma unroll
+            for (int r = 0; r < R; ++r) qr[r] = rms_norm8<LPK>(qr[r], w, p.eps, D);
+        }
 #pragma unroll
         for (int r = 0; r < R; ++r) qr[r] = rope_half8(qr[r], xor8_u4(qr[r]), cv, sv, cl < 8);
         if (with_new && wave == 0 && grp == 0) {
-            // lanes 0..15 hold the whole row, so the half exchange sees every partner
-            const U4 kn = rope_half8(nk, xor8_u4(nk), cv, sv, cl < 8);
+            // lanes 0..15 hold the whole row, so the half exchange (and the norm's row sum)
+            // sees every element
+            U4 kx = nk;
+            if (p.knw) kx = rms_norm8<LPK>(nk, load16(p.knw + cl * 16), p.eps, D);
+            const U4 kn = rope_half8(kx, xor8_u4(kx), cv, sv, cl < 8);
             buffer_store16(krs, (uint32_t)((L - 1) * kst) + cl * 16, kn);
             buffer_store16(vrs, (uint32_t)((L - 1) * vst) + cl * 16, nv);
             sm_new[0][cl] = kn;
@@ -635,6 +671,17 @@ extern "C" int q3t_decode_attention(const q3t_decode_args *a, void *stream) {
     p.cs = (const char *)a->cos; p.sn = (const char *)a->sin; p.cs_sb = a->cs_stride_b;
     p.counters = (int *)ws;
     p.partials = (float *)(ws + counters_bytes());
+    p.qnw = nullptr;
+    p.knw = nullptr;
+    p.eps = a->norm_eps;
+    if (a->q_norm_weight || a->k_norm_weight) {
+        if (!fused || !(a->norm_eps >= 0.f)) return Q3T_EINVAL;
+        if ((a->q_norm_weight && !aligned(a->q_norm_weight, 16)) ||
+            (a->k_norm_weight && !aligned(a->k_norm_weight, 16)))
+            return Q3T_EINVAL;
+        p.qnw = (const char *)a->q_norm_weight;
+        p.knw = (const char *)a->k_norm_weight;
+    }
 
     const int g = (int)(a->q_heads / a->kv_heads);
     const int sq = (int)a->query_len;

@@ -21,6 +21,12 @@ signature compatibility):
   every position at s + 1;
 * every other call rotates q/k with ``rotary`` (bf16-exact to torch eager), lets the cache
   update and calls ``attention`` (the npu_attention.attention drop-in).
+
+``fused_qk_norm=True`` (an extension, off by default) also moves the module's q_norm /
+k_norm (RMSNorm over head_dim, packed_attention.py:42-45) into that fused launch: the raw
+projection rows go in, and the per-layer chain of norm kernels disappears.  The norm's fp32
+row sums then follow the kernel's order, so normalised rows can differ from the module's in
+the last bf16 bit (the reference's own norm runs with yet another order on its device).
 """
 from __future__ import annotations
 
@@ -48,7 +54,8 @@ def _section_axes(head_dim, sections, interleaved, device):
 
 class PackedAttention(torch.nn.Module):
     def __init__(self, reference, native_gqa=False, text_only_rope=False, reference_single=False,
-                 native_rope=False, native_rope_scope="all", triton_talker_rope=False):
+                 native_rope=False, native_rope_scope="all", triton_talker_rope=False,
+                 fused_qk_norm=False):
         super().__init__()
         self.reference = reference
         projections = [reference.q_proj, reference.k_proj, reference.v_proj]
@@ -73,6 +80,23 @@ class PackedAttention(torch.nn.Module):
         self.reference_single = reference_single
         self.text_only_rope = text_only_rope
         self._axes = None
+        self._norms = self._fusable_norms(reference) if fused_qk_norm else None
+
+    @staticmethod
+    def _fusable_norms(reference):
+        """(q weight, k weight, eps) when both norms are plain RMSNorms over head_dim with bf16
+        weights and one epsilon, else None (the module's own norms run)."""
+        norms = []
+        for norm in (reference.q_norm, reference.k_norm):
+            weight = getattr(norm, 'weight', None)
+            eps = getattr(norm, 'variance_epsilon', getattr(norm, 'eps', None))
+            if (weight is None or eps is None or weight.dtype != torch.bfloat16
+                    or tuple(weight.shape) != (reference.head_dim,)):
+                return None
+            norms.append((weight, float(eps)))
+        if norms[0][1] != norms[1][1]:
+            return None
+        return norms[0][0], norms[1][0], norms[0][1]
 
     def _tables(self, position_embeddings, batch, length):
         """cos/sin as contiguous (batch, length, head_dim) rows."""
@@ -117,17 +141,24 @@ class PackedAttention(torch.nn.Module):
         heads = (*shape, -1, reference.head_dim)
         projected = torch.nn.functional.linear(hidden_states, self.weight, self.bias)
         query, key, value = projected.split(self.sizes, dim=-1)
-        query = reference.q_norm(query.reshape(heads))     # BSND
-        key = reference.k_norm(key.reshape(heads))
-        value = value.reshape(heads)
+        query, key, value = query.reshape(heads), key.reshape(heads), value.reshape(heads)  # BSND
         cos, sin = self._tables(position_embeddings, batch, length)
 
         fused = self._fused_target(past_key_values, attention_mask, batch, length, query)
         if fused is not None:
             keys, values, positions = fused
-            output = decode_step(query, key, value, keys, values, positions, cos[:, 0], sin[:, 0],
-                                 scale=reference.scaling)
+            if self._norms is not None and self._norms[0].device == query.device:
+                q_weight, k_weight, eps = self._norms
+                output = decode_step(query, key, value, keys, values, positions, cos[:, 0], sin[:, 0],
+                                     scale=reference.scaling, q_norm_weight=q_weight,
+                                     k_norm_weight=k_weight, norm_eps=eps)
+            else:
+                output = decode_step(reference.q_norm(query), reference.k_norm(key), value, keys, values,
+                                     positions, cos[:, 0], sin[:, 0], scale=reference.scaling)
             return reference.o_proj(output.reshape(*shape, -1)), None
+
+        query = reference.q_norm(query)
+        key = reference.k_norm(key)
 
         query = rotary(query.contiguous(), cos, sin).transpose(1, 2)
         key = rotary(key.contiguous(), cos, sin).transpose(1, 2)
@@ -149,7 +180,8 @@ class PackedAttention(torch.nn.Module):
 
 
 def install_packed_attention(model, native_gqa=False, text_only_rope=False, reference_single=False,
-                             native_rope=False, native_rope_scope="all", triton_talker_rope=False):
+                             native_rope=False, native_rope_scope="all", triton_talker_rope=False,
+                             fused_qk_norm=False):
     """Swap every Qwen3-TTS attention module of ``model`` for a PackedAttention."""
     replacements = []
     for parent in list(model.modules()):
@@ -159,7 +191,8 @@ def install_packed_attention(model, native_gqa=False, text_only_rope=False, refe
                 setattr(parent, name, PackedAttention(
                     child, native_gqa=native_gqa, text_only_rope=text_only_rope,
                     reference_single=reference_single, native_rope=native_rope,
-                    native_rope_scope=native_rope_scope, triton_talker_rope=triton_talker_rope))
+                    native_rope_scope=native_rope_scope, triton_talker_rope=triton_talker_rope,
+                    fused_qk_norm=fused_qk_norm))
     return replacements
 
 

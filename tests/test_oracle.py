@@ -13,6 +13,7 @@ import torch
 from oracle import attention as oatt
 from oracle import bf16 as obf16
 from oracle import kv as okv
+from oracle import norm as onorm
 from oracle import rope as orope
 from oracle import scheduler as osched
 
@@ -372,3 +373,41 @@ def test_reference_scheduler_invariants_on_a_trace():
         for op in ops:
             if op[0] == 'move':
                 assert op[1] > op[2]
+
+
+# ---- RMSNorm (q_norm / k_norm) -----------------------------------------------------------
+
+def _torch_rms_norm(x, weight, eps):
+    """The module formula in torch (CPU): fp32 row statistic, bf16 round, bf16 weight."""
+    y = x.float()
+    y = y * torch.rsqrt(y.pow(2).mean(-1, keepdim=True) + eps)
+    return weight * y.to(torch.bfloat16)
+
+
+def test_rms_norm_matches_torch_module_formula():
+    """Within one bf16 step of torch's CPU evaluation everywhere, and bit-equal for all but a
+    sliver of elements (those next to a rounding tie, where the fp32 sum order decides)."""
+    gen = torch.Generator().manual_seed(4)
+    x = (torch.randn(4096, 128, generator=gen) * 3).bfloat16()
+    w = (torch.rand(128, generator=gen) * 2 + 0.25).bfloat16()
+    got = onorm.rms_norm_bf16(_torch_bits(x).reshape(4096, 128), _torch_bits(w), 1e-6)
+    want = _torch_bits(_torch_rms_norm(x, w, 1e-6)).reshape(4096, 128)
+    gv, wv = obf16.from_bits(got), obf16.from_bits(want)
+    step = np.abs(wv) * 2.0 ** -7 + 1e-30
+    assert np.all(np.abs(gv - wv) <= step)
+    assert np.mean(got == want) > 0.995
+
+
+def test_rms_norm_closed_forms():
+    """A constant row normalises to sign * weight (up to eps); scaling the row by a power of
+    two leaves the result unchanged; a zero row stays zero."""
+    w = obf16.to_bits(np.linspace(0.5, 2.0, 128).astype(np.float32))
+    row = obf16.to_bits(np.full((1, 128), -3.0, dtype=np.float32))
+    out = obf16.from_bits(onorm.rms_norm_bf16(row, w, 0.0))
+    assert np.array_equal(out, -obf16.from_bits(w)[None])
+    rng = np.random.default_rng(5)
+    x = obf16.to_bits(rng.standard_normal((64, 128)).astype(np.float32))
+    x4 = obf16.to_bits(obf16.from_bits(x) * 4.0)
+    assert np.array_equal(onorm.rms_norm_bf16(x, w, 0.0), onorm.rms_norm_bf16(x4, w, 0.0))
+    zero = np.zeros((1, 128), dtype=np.uint16)
+    assert np.all(obf16.from_bits(onorm.rms_norm_bf16(zero, w, 1e-6)) == 0)
