@@ -275,6 +275,9 @@ def main():
     parser.add_argument("--calibrate-bytes", type=int, default=0,
                         help="after timing, launch the plain copy kernel on this many bytes "
                              "(HBM counter calibration under rocprofv3)")
+    parser.add_argument("--decode-only", action="store_true",
+                        help="skip the prefill, predictor, arena-move and talker-step details "
+                             "(per-kernel profiling of the headline launches alone)")
     parser.add_argument("--prefill-only", action="store_true",
                         help="run only the prefill workload and print its detail line "
                              "(for per-kernel profiling of the prefill kernels)")
@@ -365,11 +368,14 @@ def main():
                 raise RuntimeError("calibration copy failed")
         torch.cuda.synchronize()
 
-    prefill = prefill_detail(pkg, device)
-    predictor = predictor_detail(pkg, device)
-    moves = arena_move_detail(pkg, arena, contexts)
-    talker_step = slot_graph_detail(pkg, device, contexts)
-    talker_step_fused_norm = slot_graph_detail(pkg, device, contexts, fused_qk_norm=True)
+    extra = {}
+    if not args.decode_only:
+        extra = {"prefill": prefill_detail(pkg, device),
+                 "predictor": predictor_detail(pkg, device),
+                 "arena_move": arena_move_detail(pkg, arena, contexts),
+                 "talker_attention_step": slot_graph_detail(pkg, device, contexts),
+                 "talker_attention_step_fused_qk_norm": slot_graph_detail(pkg, device, contexts,
+                                                                          fused_qk_norm=True)}
     traffic = read_traffic()
     result = {
         "metric": "decode-attn tokens/s + achieved HBM GB/s, 64-req ragged talker step, 1 GPU",
@@ -399,11 +405,7 @@ def main():
                    "attention_only_GBs": attention_bytes(contexts) / (attn_us * 1e-6) / 1e9,
                    "max_chunks": args.max_chunks,
                    "wall_s_timed_region": wall,
-                   "prefill": prefill,
-                   "predictor": predictor,
-                   "arena_move": moves,
-                   "talker_attention_step": talker_step,
-                   "talker_attention_step_fused_qk_norm": talker_step_fused_norm},
+                   **extra},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
