@@ -162,7 +162,7 @@ typedef struct q3t_decode_args {
     void *workspace;
     int64_t workspace_bytes;
     int64_t max_chunks;      /* chunks per request and KV head, <= 1024; <= 0: enough for
-                                about 2048 workgroups over the batch */
+                                about 512 workgroups over the batch */
     /* fused only, optional: RMSNorm of the query rows / the new key rows before RoPE (the
        q_norm / k_norm of the attention module, packed_attention.py:42-45):
        bf16(weight * bf16(x * rsqrt(mean(x^2) + norm_eps))) with the fp32 sum of squares of a

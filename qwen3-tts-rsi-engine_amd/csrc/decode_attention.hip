@@ -537,10 +537,13 @@ decode_attention_kernel(DecodeParams p) {
 constexpr int64_t kMaxCounters = 65536;  // batch * kv_heads
 static int64_t counters_bytes() { return kMaxCounters * 4; }
 
-// Chunks per (request, KV head): ceil(ctx / 64) at most; by default as many as keep about
-// kTargetGroups workgroups in flight for the whole batch (fewer chunks mean fewer partial
-// states to merge, more mean more parallelism for small batches).
-constexpr int64_t kTargetGroups = 2048;
+// Chunks per (request, KV head): ceil(ctx / 64) at most; by default as many as give about
+// kTargetGroups workgroups for the whole batch, two per CU of the MI355X.  Measured over
+// 8 ... 128 requests (contexts U[64, 1024]), this count was the fastest at every batch size:
+// fewer chunks leave small batches without parallelism, more add chunk states to merge
+// and merge chains at the end of the launch (a 64-request batch runs with one chunk, no
+// merge at all).
+constexpr int64_t kTargetGroups = 512;
 static int64_t chunk_count(int64_t batch, int64_t kv_heads, int64_t ctx, int64_t max_chunks) {
     const int64_t blocks = (ctx + kChunkRows - 1) / kChunkRows;
     if (max_chunks <= 0) {

@@ -75,8 +75,10 @@ def test_rejected_calls_return_negative_status_without_a_gpu(pkg):
     assert lib.q3t_decode_attention(args, None) == -1   # more chunks than supported
     # 256 KiB of counters, then one (G * query_len) x (head_dim + 2) fp32 state per chunk:
     # ctx 1024 is 16 blocks of 64 keys; chunks are capped by max_chunks, by default at
-    # ceil(2048 / (batch * kv_heads)) (4 for 64 requests and 8 KV heads, 16 for 2 requests)
-    assert lib.q3t_decode_workspace_bytes(64, 1, 16, 8, 128, 1024, 0) == 65536 * 4 + 64 * 8 * 4 * 2 * 130 * 4
+    # ceil(512 / (batch * kv_heads)) (1 for 64 requests and 8 KV heads, 8 for 8 requests, all
+    # 16 blocks for 2 requests)
+    assert lib.q3t_decode_workspace_bytes(64, 1, 16, 8, 128, 1024, 0) == 65536 * 4 + 64 * 8 * 1 * 2 * 130 * 4
+    assert lib.q3t_decode_workspace_bytes(8, 1, 16, 8, 128, 1024, 0) == 65536 * 4 + 8 * 8 * 8 * 2 * 130 * 4
     assert lib.q3t_decode_workspace_bytes(2, 1, 16, 8, 128, 1024, 0) == 65536 * 4 + 2 * 8 * 16 * 2 * 130 * 4
     assert lib.q3t_decode_workspace_bytes(64, 2, 16, 8, 128, 1024, 4) == 65536 * 4 + 64 * 8 * 4 * 4 * 130 * 4
     assert lib.q3t_decode_workspace_bytes(64, 1, 16, 8, 128, 1024, 1025) == -1
