@@ -398,7 +398,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS,
                      "traffic": traffic},
-        "detail": {"kernel": "decode_attention_kernel<bf16,128,G2,SQ1,fused>",
+        "detail": {"kernel": "decode_attention_kernel<bf16,128,G2,SQ1,fused,streamed>",
                    "algorithmic_bytes_per_launch": bytes_per_launch,
                    "us_per_layer_launch": launch_us,
                    "us_per_layer_attention_only": attn_us,

@@ -19,7 +19,8 @@
 //   * blockIdx.x % kv_heads is the KV head, so with 8 KV heads each head maps to one XCD
 //     under the round-robin dispatch, together with its partial states and counters.
 //   * lanes: 16 bytes of one key row per lane (LPK lanes per key); a pass of the workgroup
-//     reads 4 KiB of K and 4 KiB of V, all passes of a block are issued before any math.
+//     reads 4 KiB of K and 4 KiB of V, all passes of a block are issued before any math;
+//     large arenas are read with the non-temporal cache policy (each row is read once).
 //     Scores are reduced across the LPK lanes with DPP, the softmax max across a wave's lane
 //     groups with permlane swaps, and the waves' (max, sum, acc) states merge in LDS.
 //   * a request with one chunk writes its output directly.  Otherwise every chunk publishes
@@ -60,6 +61,7 @@ struct DecodeParams {
     int *counters;
     const char *qnw, *knw;  // fused: optional RMSNorm weights (bf16, D) of query / new key rows
     float eps;
+    int stream;             // read K/V rows with the non-temporal cache policy (host choice)
 };
 
 Q3T_DEVICE int mask_elem_size(int dtype) { return dtype == Q3T_F32 ? 4 : dtype == Q3T_BOOL ? 1 : 2; }
@@ -244,7 +246,7 @@ struct DecodeShape {
 // which they meet without spilling; wider variants keep the compiler's choice.
 constexpr int decode_waves_per_eu(int es, int rows) { return es == 2 && rows <= 2 ? 6 : 1; }
 
-template <typename T, int D, int G, int SQ, bool FUSED, bool MASK>
+template <typename T, int D, int G, int SQ, bool FUSED, bool MASK, bool STREAM>
 __global__ void __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(decode_waves_per_eu(sizeof(T), G * SQ))))
 decode_attention_kernel(DecodeParams p) {
@@ -404,8 +406,13 @@ decode_attention_kernel(DecodeParams p) {
             const bool ok = j < jend;
             const uint32_t ko = ok ? (uint32_t)(j * kst) + cl * 16 : 0xfffffff0u;
             const uint32_t vo = ok ? (same_stride ? ko : (uint32_t)(j * vst) + cl * 16) : 0xfffffff0u;
-            kr[pp] = buffer_load16(krs, ko);
-            vr[pp] = buffer_load16(vrs, vo);
+            if constexpr (STREAM) {
+                kr[pp] = buffer_load16_stream(krs, ko);
+                vr[pp] = buffer_load16_stream(vrs, vo);
+            } else {
+                kr[pp] = buffer_load16(krs, ko);
+                vr[pp] = buffer_load16(vrs, vo);
+            }
         }
     };
     auto block_keys = [&](int jb, int (&kidx)[P], bool (&valid)[P]) {
@@ -544,6 +551,16 @@ static int64_t counters_bytes() { return kMaxCounters * 4; }
 // and merge chains at the end of the launch (a 64-request batch runs with one chunk, no
 // merge at all).
 constexpr int64_t kTargetGroups = 512;
+
+// K/V rows are read with the non-temporal policy when the launch may read more than
+// kStreamBytes of them: a talker arena layer (64 requests x 1024 rows: 268 MB) is read once
+// per step, so caching it only evicts other data (10% faster streamed at 8-128 requests);
+// a code-predictor cache (64 requests x 16 rows: 4 MB per layer) is re-read by the next
+// step and stays cached (7% slower streamed).
+constexpr int64_t kStreamBytes = 16 << 20;
+static int stream_kv(int64_t batch, int64_t kv_heads, int64_t ctx, int64_t row_bytes) {
+    return batch * kv_heads * ctx * row_bytes * 2 >= kStreamBytes ? 1 : 0;
+}
 static int64_t chunk_count(int64_t batch, int64_t kv_heads, int64_t ctx, int64_t max_chunks) {
     const int64_t blocks = (ctx + kChunkRows - 1) / kChunkRows;
     if (max_chunks <= 0) {
@@ -570,8 +587,15 @@ extern "C" int64_t q3t_decode_workspace_bytes(int64_t batch, int64_t query_len, 
 
 template <typename T, int D, int G, int SQ, bool F, bool M>
 static void launch_decode(const DecodeParams &p, hipStream_t s) {
-    hipLaunchKernelGGL((decode_attention_kernel<T, D, G, SQ, F, M>),
-                       dim3((uint32_t)p.B * p.Hkv * p.nchunks), dim3(kThreads), 0, s, p);
+    const dim3 grid((uint32_t)p.B * p.Hkv * p.nchunks);
+    // streamed instances only for the talker-shaped single-query launches without a mask
+    if constexpr (sizeof(T) == 2 && D == 128 && SQ == 1 && !M) {
+        if (p.stream) {
+            hipLaunchKernelGGL((decode_attention_kernel<T, D, G, SQ, F, M, true>), grid, dim3(kThreads), 0, s, p);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((decode_attention_kernel<T, D, G, SQ, F, M, false>), grid, dim3(kThreads), 0, s, p);
 }
 
 template <typename T, int D, int G>
@@ -655,6 +679,7 @@ extern "C" int q3t_decode_attention(const q3t_decode_args *a, void *stream) {
     p.Hkv = (int)a->kv_heads;
     p.ctx = (int)a->ctx;
     p.nchunks = (int)nchunks;
+    p.stream = stream_kv(a->batch, a->kv_heads, a->ctx, a->head_dim * es);
     p.scale_log2 = a->scale * kLog2e;
     p.has_mask = a->mask != nullptr;
     p.mask_dtype = (int)a->mask_dtype;
