@@ -107,15 +107,14 @@ def prefill_detail(pkg, device, reps=20):
 def predictor_detail(pkg, device, reps=20):
     """The code predictor's attention: 64 requests, 5 layers, 15 steps over a 16-position
     cache (PredictorCache windows: step 0 writes positions 0-1 and attends them causally,
-    step s writes s+1 and attends 0..s+1).  Step 0 is the two-token write + masked-causal
-    decode; steps 1-14 are fused one-token launches.  All 75 layer-steps in one graph."""
+    step s writes s+1 and attends 0..s+1).  Every layer-step is one fused launch (two tokens
+    at step 0, one after); all 75 in one graph."""
     layers, steps, batch, cap = 5, 15, BATCH, 16
     dgen = torch.Generator(device=device).manual_seed(3)
     arena = torch.zeros(2 * layers, batch, HKV, cap, D, device=device, dtype=torch.bfloat16)
     rows = torch.randn(steps, layers, batch, 2, HQ + 2 * HKV, D, generator=dgen, device=device,
                        dtype=torch.bfloat16)
     positions = [torch.full((batch,), max(s + 1, 1), device=device, dtype=torch.int64) for s in range(steps)]
-    start0 = torch.zeros(batch, device=device, dtype=torch.int64)
     tables = [pkg.rope_tables(positions[s], D) for s in range(steps)]
     cos0, sin0 = pkg.rope_tables(torch.arange(2, device=device).expand(batch, 2).contiguous(), D)
     out = torch.empty(batch, 2, HQ, D, device=device, dtype=torch.bfloat16)
@@ -126,10 +125,8 @@ def predictor_detail(pkg, device, reps=20):
                 r = rows[s, layer]
                 keys, values = arena[layer], arena[layers + layer]
                 if s == 0:
-                    q = pkg.rotary(r[:, :, :HQ].contiguous(), cos0, sin0)
-                    k = pkg.rotary(r[:, :, HQ:HQ + HKV].contiguous(), cos0, sin0)
-                    pkg.write_tokens(k.transpose(1, 2), r[:, :, HQ + HKV:].transpose(1, 2), keys, values, start0)
-                    pkg.decode_attention(q, keys, values, positions[0], out=out)
+                    pkg.decode_step(r[:, :, :HQ], r[:, :, HQ:HQ + HKV], r[:, :, HQ + HKV:], keys, values,
+                                    positions[0], cos0, sin0, out=out)
                 else:
                     q, k, v = r[:, :1, :HQ], r[:, :1, HQ:HQ + HKV], r[:, :1, HQ + HKV:]
                     pkg.decode_step(q, k, v, keys, values, positions[s], *tables[s], out=out[:, :1])

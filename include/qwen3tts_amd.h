@@ -120,11 +120,15 @@ int q3t_rope_tables(const int64_t *positions, int64_t n, const float *inv_freq, 
  * workgroup; chunks past a request's length exit at once.  A request with several chunks merges the chunks' partial softmax states
  * through `workspace`; the last chunk to finish writes the output.
  *
- * fused != 0 additionally performs, for query_len == 1:
- *   - RoPE of the query rows and of the new key with cos/sin rows (bf16-exact, as q3t_rotary),
- *   - the paired K/V write of the new (rotated) key and value at positions[b],
- * and uses the new key/value for key p_b without re-reading the arena.  Then `query`,
- * `new_key`, `new_value` are the un-rotated BSND rows of the QKV projection.
+ * fused != 0 additionally performs, for query_len S in {1, 2} (the step's tokens sit at
+ * positions p_b - S + 1 ... p_b):
+ *   - RoPE of the query rows and of the new keys with each token's cos/sin row (bf16-exact,
+ *     as q3t_rotary),
+ *   - the paired K/V write of the new (rotated) keys and values at those positions,
+ * and uses the new keys/values for those key positions without re-reading the arena; with
+ * S == 2, query token 0 does not attend key p_b (the code predictor's first step with its
+ * 2x2 causal mask, continuous.py:39-40).  Then `query`, `new_key`, `new_value` are the
+ * un-rotated BSND rows of the QKV projection.
  * Replaces: PackedAttention.forward's RoPE + cache update + attention dispatch
  * (packed_attention.py:46-84), npu_attention.attention (npu_attention.py:11-26).
  */
@@ -151,7 +155,8 @@ typedef struct q3t_decode_args {
     /* output (batch, query_len, q_heads, head_dim), same dtype as query */
     void *out;
     int64_t o_stride_b, o_stride_s, o_stride_h;
-    /* fused only: new key/value rows (batch, kv_heads, head_dim) and cos/sin (batch, head_dim) */
+    /* fused only: new key/value rows (batch, S, kv_heads, head_dim) and cos/sin
+       (batch, S, head_dim); the token strides are the last fields below */
     const void *new_key, *new_value;
     int64_t nk_stride_b, nk_stride_h, nv_stride_b, nv_stride_h;
     const void *cos, *sin;
@@ -169,6 +174,8 @@ typedef struct q3t_decode_args {
        row; weights are bf16 (head_dim,); NULL = that row is used as given */
     const void *q_norm_weight, *k_norm_weight;
     float norm_eps;
+    /* fused, S == 2: token strides of new_key, new_value and cos/sin (elements) */
+    int64_t nk_stride_s, nv_stride_s, cs_stride_s;
 } q3t_decode_args;
 
 /* Bytes of workspace needed by q3t_decode_attention for these sizes. */

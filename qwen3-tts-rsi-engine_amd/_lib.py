@@ -47,6 +47,7 @@ class DecodeArgs(ctypes.Structure):
         ("cos", c_vp), ("sin", c_vp), ("cs_stride_b", c_i64),
         ("workspace", c_vp), ("workspace_bytes", c_i64), ("max_chunks", c_i64),
         ("q_norm_weight", c_vp), ("k_norm_weight", c_vp), ("norm_eps", ctypes.c_float),
+        ("nk_stride_s", c_i64), ("nv_stride_s", c_i64), ("cs_stride_s", c_i64),
     ]
 
 
@@ -106,6 +107,9 @@ class KernelError(RuntimeError):
     """A HIP launch failed after host validation passed."""
 
 
+ABI_VERSION = 2  # q3t_abi_version() of the header these structures mirror
+
+
 def library() -> ctypes.CDLL:
     """Load the HIP library once; raise if it has not been built."""
     global _lib
@@ -121,6 +125,9 @@ def library() -> ctypes.CDLL:
                 fn = getattr(lib, name)
                 fn.restype = restype
                 fn.argtypes = argtypes
+            if lib.q3t_abi_version() != ABI_VERSION:
+                raise RuntimeError(f"{LIBRARY_PATH.name} implements ABI {lib.q3t_abi_version()}, "
+                                   f"these bindings ABI {ABI_VERSION}; rebuild it")
             _lib = lib
     return _lib
 

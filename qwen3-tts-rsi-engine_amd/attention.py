@@ -126,20 +126,23 @@ def decode_attention(query, keys, values, positions, *, scale=None, mask=None, k
 def decode_step(query, new_key, new_value, key_arena, value_arena, positions, cos, sin, *,
                 scale=None, out=None, max_chunks=0, q_norm_weight=None, k_norm_weight=None,
                 norm_eps=1e-6):
-    """Fused one-token decode for a layer.
+    """Fused decode step of a layer for one token, or two (the code predictor's first step).
 
-    query (B, 1, Hq, D), new_key/new_value (B, 1, Hkv, D): un-rotated bf16 rows (views of the
-    fused QKV projection are fine); key_arena/value_arena (slots >= B, Hkv, C, D) contiguous;
-    positions (B,) int64; cos/sin (B, D) or (B, 1, D) bf16.  Writes the rotated key and the
-    value at positions[b] and returns the attention output (B, 1, Hq, D).
+    query (B, S, Hq, D), new_key/new_value (B, S, Hkv, D) with S in {1, 2}: un-rotated bf16
+    rows (views of the fused QKV projection are fine); key_arena/value_arena (slots >= B, Hkv,
+    C, D) contiguous; positions (B,) int64, the position of the step's last token; cos/sin
+    (B, S, D), or (B, D) for one token, bf16.  Writes the rotated keys and the values at
+    positions[b] - S + 1 ... positions[b] and returns the attention output (B, S, Hq, D); with
+    two tokens the first does not attend the second (2x2 causal, continuous.py:39-40).
 
     With ``q_norm_weight`` / ``k_norm_weight`` (bf16 (D,)) the query / key rows are first
     RMS-normalised in the kernel (the module's q_norm / k_norm, eps ``norm_eps``): raw
     projection rows go in and no separate norm kernels run.  The fp32 row sums follow the
     kernel's order, so a result can differ from another implementation's in the last bf16 bit."""
-    if query.ndim != 4 or query.shape[1] != 1 or new_key.ndim != 4 or new_key.shape[1] != 1:
-        raise ValueError('fused decode expects one-token BSND rows')
-    batch, _, q_heads, head_dim = query.shape
+    if (query.ndim != 4 or query.shape[1] not in (1, 2) or new_key.ndim != 4
+            or new_key.shape[1] != query.shape[1]):
+        raise ValueError('fused decode expects one- or two-token BSND rows')
+    batch, tokens, q_heads, head_dim = query.shape
     if new_value.shape != new_key.shape or new_key.shape[0] != batch or new_key.shape[3] != head_dim:
         raise ValueError('new key/value rows must match the query batch and head_dim')
     kv_heads = new_key.shape[2]
@@ -154,17 +157,18 @@ def decode_step(query, new_key, new_value, key_arena, value_arena, positions, co
         raise ValueError('fused decode is bf16-only (exact RoPE rounding contract)')
     if positions.shape != (batch,) or positions.dtype != torch.int64:
         raise ValueError('positions must be an int64 (batch,) tensor')
-    cos2 = cos.reshape(cos.shape[0], -1) if cos.ndim == 3 else cos
-    sin2 = sin.reshape(sin.shape[0], -1) if sin.ndim == 3 else sin
-    if cos2.shape != (batch, head_dim) or sin2.shape != cos2.shape or cos2.stride(1) != 1 or sin2.stride() != cos2.stride():
-        raise ValueError('cos/sin must be (B, head_dim) rows')
+    cos3 = cos[:, None] if cos.ndim == 2 else cos
+    sin3 = sin[:, None] if sin.ndim == 2 else sin
+    if (cos3.shape != (batch, tokens, head_dim) or sin3.shape != cos3.shape or cos3.stride(2) != 1
+            or sin3.stride() != cos3.stride()):
+        raise ValueError('cos/sin must be (B, S, head_dim) rows')
     if any(t.stride(3) != 1 for t in (query, new_key, new_value)):
         raise ValueError('rows must be unit-stride along head_dim')
     device = _lib.require_gpu(*tensors, positions)
     if out is None:
-        out = torch.empty(batch, 1, q_heads, head_dim, device=device, dtype=query.dtype)
+        out = torch.empty(batch, tokens, q_heads, head_dim, device=device, dtype=query.dtype)
     a = _lib.DecodeArgs()
-    a.batch, a.query_len, a.q_heads, a.kv_heads, a.head_dim = batch, 1, q_heads, kv_heads, head_dim
+    a.batch, a.query_len, a.q_heads, a.kv_heads, a.head_dim = batch, tokens, q_heads, kv_heads, head_dim
     a.ctx = key_arena.shape[2]
     a.dtype = _lib.Q3T_BF16
     a.scale = head_dim ** -0.5 if scale is None else float(scale)
@@ -178,10 +182,10 @@ def decode_step(query, new_key, new_value, key_arena, value_arena, positions, co
     a.out = out.data_ptr()
     a.o_stride_b, a.o_stride_s, a.o_stride_h = out.stride()[:3]
     a.new_key, a.new_value = new_key.data_ptr(), new_value.data_ptr()
-    a.nk_stride_b, a.nk_stride_h = new_key.stride(0), new_key.stride(2)
-    a.nv_stride_b, a.nv_stride_h = new_value.stride(0), new_value.stride(2)
-    a.cos, a.sin = cos2.data_ptr(), sin2.data_ptr()
-    a.cs_stride_b = cos2.stride(0)
+    a.nk_stride_b, a.nk_stride_s, a.nk_stride_h = new_key.stride()[:3]
+    a.nv_stride_b, a.nv_stride_s, a.nv_stride_h = new_value.stride()[:3]
+    a.cos, a.sin = cos3.data_ptr(), sin3.data_ptr()
+    a.cs_stride_b, a.cs_stride_s = cos3.stride(0), cos3.stride(1)
     a.max_chunks = int(max_chunks)
     for name, weight in (('q_norm_weight', q_norm_weight), ('k_norm_weight', k_norm_weight)):
         if weight is None:

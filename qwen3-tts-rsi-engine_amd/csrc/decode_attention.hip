@@ -7,7 +7,9 @@
 //   npu_attention.attention, npu_attention.py:11-26).
 // Fused variant: RoPE of q and of the new key (packed_attention.py:46-51,
 // rotary_triton_ascend.py:19-24) and the paired K/V write at pos[b]
-// (continuous.py:152-166, kv_triton_ascend.py:24-36) happen inside the same launch.
+// (continuous.py:152-166, kv_triton_ascend.py:24-36) happen inside the same launch; with
+// two tokens per request (the code predictor's first step, continuous.py:37-40) both are
+// rotated, written at pos[b] - 1 and pos[b], and attended causally.
 //
 // Design (one launch per layer, no per-step preparation):
 //   * keys are cut into chunks of kChunkRows consecutive keys (several consecutive blocks
@@ -62,6 +64,7 @@ struct DecodeParams {
     const char *qnw, *knw;  // fused: optional RMSNorm weights (bf16, D) of query / new key rows
     float eps;
     int stream;             // read K/V rows with the non-temporal cache policy (host choice)
+    int64_t nk_ss, nv_ss, cs_ss;  // fused, two tokens: token strides of new K/V and cos/sin
 };
 
 Q3T_DEVICE int mask_elem_size(int dtype) { return dtype == Q3T_F32 ? 4 : dtype == Q3T_BOOL ? 1 : 2; }
@@ -253,11 +256,11 @@ decode_attention_kernel(DecodeParams p) {
     constexpr int R = G * SQ;
     using S = DecodeShape<T, D>;
     constexpr int LPK = S::LPK, CW = S::CW, RPW = S::RPW, RPP = S::RPP, P = S::P, ES = S::ES;
-    static_assert(!FUSED || (ES == 2 && D == 128 && SQ == 1), "fused path: bf16, D=128, one query");
+    static_assert(!FUSED || (ES == 2 && D == 128 && SQ <= 2), "fused path: bf16, D=128, one or two tokens");
 
     __shared__ float sm_acc[kWaves][R][D];
     __shared__ float sm_ml[kWaves][R][2];
-    __shared__ U4 sm_new[FUSED ? 2 : 1][16];
+    __shared__ U4 sm_new[FUSED ? 2 : 1][FUSED ? SQ : 1][16];  // rotated new keys, new values
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int grp = lane / LPK, cl = lane % LPK;
@@ -266,17 +269,25 @@ decode_attention_kernel(DecodeParams p) {
     const int c = rest % p.nchunks, b = rest / p.nchunks;
 
     // what depends only on (request, head) is requested together with the position: the query
-    // rows and, fused, the cos/sin row and the new key/value rows (16 bytes per lane each)
+    // rows and, fused, the cos/sin rows of the step's tokens and the new key/value rows (16
+    // bytes per lane each; lane group t holds token t's new rows)
     const int64_t pb = p.pos[b];
     U4 qr[R];
-    U4 nk, nv, cv, sv;
+    U4 nk, nv, cv[SQ], sv[SQ];
     if constexpr (FUSED) {
-        cv = load16(p.cs + b * p.cs_sb * 2 + cl * 16);
-        sv = load16(p.sn + b * p.cs_sb * 2 + cl * 16);
 #pragma unroll
-        for (int r = 0; r < R; ++r) qr[r] = load16(p.q + (b * p.q_sb + (h * G + r) * p.q_sh) * ES + cl * 16);
-        nk = load16(p.nk + (b * p.nk_sb + h * p.nk_sh) * ES + cl * 16);
-        nv = load16(p.nv + (b * p.nv_sb + h * p.nv_sh) * ES + cl * 16);
+        for (int t = 0; t < SQ; ++t) {
+            cv[t] = load16(p.cs + (b * p.cs_sb + t * p.cs_ss) * 2 + cl * 16);
+            sv[t] = load16(p.sn + (b * p.cs_sb + t * p.cs_ss) * 2 + cl * 16);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int qi = r / G, hq = h * G + r % G;
+            qr[r] = load16(p.q + (b * p.q_sb + qi * p.q_ss + hq * p.q_sh) * ES + cl * 16);
+        }
+        const int tk = grp < SQ ? grp : SQ - 1;
+        nk = load16(p.nk + (b * p.nk_sb + tk * p.nk_ss + h * p.nk_sh) * ES + cl * 16);
+        nv = load16(p.nv + (b * p.nv_sb + tk * p.nv_ss + h * p.nv_sh) * ES + cl * 16);
     } else {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -300,9 +311,10 @@ decode_attention_kernel(DecodeParams p) {
     if (c >= n) return;
     const int j0 = c * per * kChunkRows;
     const int j1 = min(L, j0 + per * kChunkRows);
-    // fused: key L-1 is the new key; the last chunk writes it and attends it from LDS
+    // fused: keys L-SQ ... L-1 are the step's new keys; the last chunk writes them and attends
+    // them from LDS, no chunk reads them from the arena
     const bool with_new = FUSED && c == n - 1;
-    const int jend = with_new ? L - 1 : j1;  // arena keys of this chunk: [j0, jend)
+    const int jend = FUSED ? min(j1, L - SQ) : j1;  // arena keys of this chunk: [j0, jend)
 
     const char *kb = p.k + ((p.offs ? p.offs[b] : (int64_t)b * p.k_sb) + h * p.k_sh) * ES;
     const char *vb = p.v + ((p.offs ? p.offs[b] : (int64_t)b * p.v_sb) + h * p.v_sh) * ES;
@@ -319,17 +331,20 @@ decode_attention_kernel(DecodeParams p) {
             for (int r = 0; r < R; ++r) qr[r] = rms_norm8<LPK>(qr[r], w, p.eps, D);
         }
 #pragma unroll
-        for (int r = 0; r < R; ++r) qr[r] = rope_half8(qr[r], xor8_u4(qr[r]), cv, sv, cl < 8);
-        if (with_new && wave == 0 && grp == 0) {
-            // lanes 0..15 hold the whole row, so the half exchange (and the norm's row sum)
-            // sees every element
+        for (int r = 0; r < R; ++r) qr[r] = rope_half8(qr[r], xor8_u4(qr[r]), cv[r / G], sv[r / G], cl < 8);
+        if (with_new && wave == 0 && grp < SQ && L - SQ + grp >= 0) {
+            // lane group t of wave 0 holds token t's whole rows, so the half exchange (and the
+            // norm's row sum) sees every element
+            const U4 ct = SQ == 1 || grp == 0 ? cv[0] : cv[SQ - 1];
+            const U4 st = SQ == 1 || grp == 0 ? sv[0] : sv[SQ - 1];
             U4 kx = nk;
             if (p.knw) kx = rms_norm8<LPK>(nk, load16(p.knw + cl * 16), p.eps, D);
-            const U4 kn = rope_half8(kx, xor8_u4(kx), cv, sv, cl < 8);
-            buffer_store16(krs, (uint32_t)((L - 1) * kst) + cl * 16, kn);
-            buffer_store16(vrs, (uint32_t)((L - 1) * vst) + cl * 16, nv);
-            sm_new[0][cl] = kn;
-            sm_new[1][cl] = nv;
+            const U4 kn = rope_half8(kx, xor8_u4(kx), ct, st, cl < 8);
+            const int row = L - SQ + grp;
+            buffer_store16(krs, (uint32_t)(row * kst) + cl * 16, kn);
+            buffer_store16(vrs, (uint32_t)(row * vst) + cl * 16, nv);
+            sm_new[0][grp][cl] = kn;
+            sm_new[1][grp][cl] = nv;
         }
     }
 
@@ -431,17 +446,18 @@ decode_attention_kernel(DecodeParams p) {
         step(kr, vr, kidx, valid, jb != j0);
     }
     if constexpr (FUSED) {
-        if (with_new && wave == 0) {  // the new key, held by lanes 0..15 of wave 0
+        if (with_new && wave == 0) {  // the new keys: token t's in lane group t of wave 0
             U4 kr[P], vr[P];
             int kidx[P];
             bool valid[P];
             const U4 zero = {0u, 0u, 0u, 0u};
+            const bool mine = grp < SQ && L - SQ + grp >= 0;
 #pragma unroll
             for (int pp = 0; pp < P; ++pp) {
-                kr[pp] = (pp == 0 && grp == 0) ? sm_new[0][cl] : zero;
-                vr[pp] = (pp == 0 && grp == 0) ? sm_new[1][cl] : zero;
-                kidx[pp] = L - 1;
-                valid[pp] = pp == 0 && grp == 0;
+                kr[pp] = (pp == 0 && mine) ? sm_new[0][grp < SQ ? grp : 0][cl] : zero;
+                vr[pp] = (pp == 0 && mine) ? sm_new[1][grp < SQ ? grp : 0][cl] : zero;
+                kidx[pp] = L - SQ + grp;
+                valid[pp] = pp == 0 && mine;
             }
             step(kr, vr, kidx, valid, j0 < jend);
         }
@@ -602,8 +618,10 @@ template <typename T, int D, int G>
 static int dispatch_sq(const DecodeParams &p, int sq, bool fused, hipStream_t s) {
     if (fused) {
         if constexpr (sizeof(T) == 2 && D == 128) {
-            if (sq != 1 || p.has_mask) return Q3T_EUNSUPPORTED;
-            launch_decode<T, D, G, 1, true, false>(p, s);
+            if (p.has_mask) return Q3T_EUNSUPPORTED;
+            if (sq == 1) launch_decode<T, D, G, 1, true, false>(p, s);
+            else if (sq == 2) launch_decode<T, D, G, 2, true, false>(p, s);
+            else return Q3T_EUNSUPPORTED;
             return Q3T_OK;
         } else {
             return Q3T_EUNSUPPORTED;
@@ -655,7 +673,8 @@ extern "C" int q3t_decode_attention(const q3t_decode_args *a, void *stream) {
         if ((st * es) % 16) return Q3T_EINVAL;
     if (!aligned(a->query, 16) || !aligned(a->keys, 16) || !aligned(a->values, 16)) return Q3T_EINVAL;
     if (fused) {
-        const int64_t fs[] = {a->nk_stride_b, a->nk_stride_h, a->nv_stride_b, a->nv_stride_h, a->cs_stride_b};
+        const int64_t fs[] = {a->nk_stride_b, a->nk_stride_h, a->nv_stride_b, a->nv_stride_h, a->cs_stride_b,
+                              a->nk_stride_s, a->nv_stride_s, a->cs_stride_s};
         for (int64_t st : fs)
             if ((st * es) % 16) return Q3T_EINVAL;
         if (!aligned(a->new_key, 16) || !aligned(a->new_value, 16) || !aligned(a->cos, 16) ||
@@ -697,6 +716,7 @@ extern "C" int q3t_decode_attention(const q3t_decode_args *a, void *stream) {
     p.nk = (const char *)a->new_key; p.nv = (const char *)a->new_value;
     p.nk_sb = a->nk_stride_b; p.nk_sh = a->nk_stride_h; p.nv_sb = a->nv_stride_b; p.nv_sh = a->nv_stride_h;
     p.cs = (const char *)a->cos; p.sn = (const char *)a->sin; p.cs_sb = a->cs_stride_b;
+    p.nk_ss = a->nk_stride_s; p.nv_ss = a->nv_stride_s; p.cs_ss = a->cs_stride_s;
     p.counters = (int *)ws;
     p.partials = (float *)(ws + counters_bytes());
     p.qnw = nullptr;

@@ -19,6 +19,11 @@ signature compatibility):
   it writes position s + 1 and attends positions 0 ... s + 1 (predictor.py:19-24, the
   unmasked steps of UniformPredictor.run, continuous.py:55-62), which is ``decode_step`` with
   every position at s + 1;
+* and the predictor's first step, two tokens under the 2x2 causal mask (continuous.py:39-40,
+  zeros with finfo.min above the diagonal, or no mask, which the attention treats as causal
+  for two queries): ``decode_step`` writes positions 0 and 1 and attends them causally.  The
+  mask's values are read once, outside graph capture, and the verdict is kept per mask
+  tensor;
 * every other call rotates q/k with ``rotary`` (bf16-exact to torch eager), lets the cache
   update and calls ``attention`` (the npu_attention.attention drop-in).
 
@@ -37,6 +42,33 @@ from .rotary import rotary
 from .slots import PredictorCache, SlotCache
 
 _ATTENTION_CLASSES = ('Qwen3TTSTalkerAttention', 'Qwen3TTSAttention')
+
+_CAUSAL_PAIR: dict = {}
+
+
+def _is_causal_pair(mask, batch):
+    """True if ``mask`` is the code predictor's first-step mask: (1 or batch, 1, 2, 2) with 0
+    on and below the diagonal and a value at or below the dtype's finfo.min above it
+    (continuous.py:39-40), or None (two queries without a mask attend causally,
+    npu_attention.py:17-18).  The values are read on the host once per tensor version
+    outside graph capture; during capture an unseen mask counts as not causal."""
+    if mask is None:
+        return True
+    if (not isinstance(mask, torch.Tensor) or mask.ndim != 4 or mask.shape[0] not in (1, batch)
+            or mask.shape[1:] != (1, 2, 2) or not mask.dtype.is_floating_point):
+        return False
+    key = (mask.data_ptr(), mask._version, tuple(mask.shape), tuple(mask.stride()), mask.dtype, mask.device)
+    seen = _CAUSAL_PAIR.get(key)
+    if seen is None:
+        if mask.is_cuda and torch.cuda.is_current_stream_capturing():
+            return False
+        values = mask.detach().float().cpu()
+        low = torch.finfo(mask.dtype).min
+        verdict = bool((values[..., 0, 0] == 0).all() and (values[..., 1, 0] == 0).all()
+                       and (values[..., 1, 1] == 0).all() and (values[..., 0, 1] <= low).all())
+        # the entry keeps the mask alive, so its address cannot be reused by another tensor
+        seen = _CAUSAL_PAIR[key] = (verdict, mask)
+    return seen[0]
 
 
 def _section_axes(head_dim, sections, interleaved, device):
@@ -116,12 +148,20 @@ class PackedAttention(torch.nn.Module):
         return cos, sin
 
     def _fused_target(self, cache, attention_mask, batch, length, query):
-        """(keys, values, positions) of a one-token step the fused launch can take, else None."""
+        """(keys, values, positions) of a step the fused launch can take, else None."""
         reference = self.reference
-        if (length != 1 or reference.training or query.dtype != torch.bfloat16
+        if (length not in (1, 2) or reference.training or query.dtype != torch.bfloat16
                 or reference.head_dim != 128):
             return None
         layer = reference.layer_idx
+        if length == 2:
+            if (isinstance(cache, PredictorCache) and cache.step == 0
+                    and _is_causal_pair(attention_mask, batch)):
+                keys, values = cache.keys[layer], cache.values[layer]
+                if (keys.is_contiguous() and values.is_contiguous() and keys.shape[0] == batch
+                        and keys.shape[2] >= 2):
+                    return keys, values, cache.positions_at(batch, 1, query.device)
+            return None
         if isinstance(cache, SlotCache):
             keys, values = cache.arena.keys[layer], cache.arena.values[layer]
             if keys.is_contiguous() and values.is_contiguous():
@@ -149,12 +189,12 @@ class PackedAttention(torch.nn.Module):
             keys, values, positions = fused
             if self._norms is not None and self._norms[0].device == query.device:
                 q_weight, k_weight, eps = self._norms
-                output = decode_step(query, key, value, keys, values, positions, cos[:, 0], sin[:, 0],
+                output = decode_step(query, key, value, keys, values, positions, cos, sin,
                                      scale=reference.scaling, q_norm_weight=q_weight,
                                      k_norm_weight=k_weight, norm_eps=eps)
             else:
                 output = decode_step(reference.q_norm(query), reference.k_norm(key), value, keys, values,
-                                     positions, cos[:, 0], sin[:, 0], scale=reference.scaling)
+                                     positions, cos, sin, scale=reference.scaling)
             return reference.o_proj(output.reshape(*shape, -1)), None
 
         query = reference.q_norm(query)

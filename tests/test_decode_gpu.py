@@ -97,6 +97,69 @@ def test_config2_fused_decode_step(pkg, device, max_chunks):
     assert_attention_close(f64(out)[:, 0], expected[:, 0])
 
 
+def _expected_fused_tokens(k, v, q, kn, vn, positions, cos, sin):
+    """Oracle chain of a fused step of S tokens at positions p - S + 1 ... p: per-token RoPE of
+    the query and key rows, the paired write, causal attention (query t sees keys <= p - S + 1 + t)."""
+    tokens = q.shape[1]
+    cb, sb = bits(cos)[:, :, None, :], bits(sin)[:, :, None, :]
+    q_rot = orope.rope_bf16(bits(q), cb, sb)
+    k_rot = orope.rope_bf16(bits(kn), cb, sb)
+    ak, av = okv.kv_write(bits(k).copy(), bits(v).copy(), k_rot.transpose(0, 2, 1, 3),
+                          bits(vn).transpose(0, 2, 1, 3), positions - tokens + 1)
+    out = oatt.decode_attention(obf16.from_bits(q_rot), obf16.from_bits(ak), obf16.from_bits(av),
+                                positions, D ** -0.5)
+    return ak, av, out
+
+
+@pytest.mark.parametrize("group", [1, 2, 4])
+@pytest.mark.parametrize("max_chunks", [0, 1, 3])
+def test_fused_two_token_step(pkg, device, group, max_chunks):
+    """The code predictor's first step as one launch (continuous.py:37-40: two tokens, 2x2
+    causal): RoPE of both tokens, the paired write at p - 1 and p, attention with query 0
+    blind to key p.  Positions include chunk boundaries (the new key p - 1 in an earlier
+    chunk than p) and the first two arena rows."""
+    kv_heads, batch, capacity = 4, 9, 300
+    q_heads = kv_heads * group
+    k, v = _arena(batch, capacity, torch.bfloat16, device, 41 + group, kv_heads=kv_heads)
+    gen = torch.Generator().manual_seed(40 + group + max_chunks)
+    positions = torch.tensor([1, 2, 63, 64, 65, 128, 200, 298, 299])
+    qkv = torch.randn(batch, 2, (q_heads + 2 * kv_heads) * D, generator=gen).bfloat16().to(device)
+    q = qkv[..., :q_heads * D].view(batch, 2, q_heads, D)
+    kn = qkv[..., q_heads * D:(q_heads + kv_heads) * D].view(batch, 2, kv_heads, D)
+    vn = qkv[..., (q_heads + kv_heads) * D:].view(batch, 2, kv_heads, D)
+    token_positions = torch.stack([positions - 1, positions], 1)
+    cos, sin = pkg.rope_tables(token_positions.to(device), D)
+    expected_k, expected_v, expected = _expected_fused_tokens(k, v, q, kn, vn, positions.numpy(), cos, sin)
+    out = pkg.decode_step(q, kn, vn, k, v, positions.to(device), cos, sin, max_chunks=max_chunks)
+    assert np.array_equal(bits(k), expected_k) and np.array_equal(bits(v), expected_v)
+    assert_attention_close(f64(out), expected)
+
+
+def test_fused_two_token_predictor_first_step(pkg, device):
+    """Batch 64, 8 KV heads, a fresh 16-position predictor cache: the first step writes rows
+    0 and 1 and attends them causally; the unfused chain (rotary, write_tokens, two-query
+    decode) gives the same cache and output."""
+    batch = 64
+    k = torch.zeros(batch, HKV, 16, D, device=device, dtype=torch.bfloat16)
+    v = torch.zeros_like(k)
+    gen = torch.Generator().manual_seed(44)
+    rows = torch.randn(batch, 2, HQ + 2 * HKV, D, generator=gen).bfloat16().to(device)
+    q, kn, vn = rows[:, :, :HQ], rows[:, :, HQ:HQ + HKV], rows[:, :, HQ + HKV:]
+    positions = torch.ones(batch, dtype=torch.int64, device=device)
+    cos, sin = pkg.rope_tables(torch.arange(2, device=device).expand(batch, 2).contiguous(), D)
+    expected_k, expected_v, expected = _expected_fused_tokens(k, v, q, kn, vn, positions.cpu().numpy(), cos, sin)
+    out = pkg.decode_step(q, kn, vn, k, v, positions, cos, sin)
+    assert np.array_equal(bits(k), expected_k) and np.array_equal(bits(v), expected_v)
+    assert_attention_close(f64(out), expected)
+    k2, v2 = torch.zeros_like(k), torch.zeros_like(v)
+    q_rot = pkg.rotary(q.contiguous(), cos, sin)
+    k_rot = pkg.rotary(kn.contiguous(), cos, sin)
+    pkg.write_tokens(k_rot.transpose(1, 2), vn.transpose(1, 2), k2, v2, torch.zeros_like(positions))
+    chain = pkg.decode_attention(q_rot, k2, v2, positions)
+    assert torch.equal(k, k2) and torch.equal(v, v2)
+    assert (out.float() - chain.float()).abs().max().item() <= 1e-2
+
+
 def test_fused_matches_unfused_chain(pkg, device):
     """rotary -> write -> decode_attention gives the same output as the fused launch."""
     contexts, k, v, q, kn, vn = _config2(device, seed=3)

@@ -145,9 +145,16 @@ def test_talker_decode_layer_through_slot_cache(pkg, device, fused_path):
         assert_attention_close(got, expected, max_abs=1e-5, mean_abs=1e-6)
 
 
-def test_predictor_first_step_two_queries_with_mask(pkg, device):
-    """Code predictor step 0: two tokens, the 2x2 causal 0/finfo.min mask
-    (continuous.py:39-40), a PredictorCache writing positions [0, 2)."""
+@pytest.mark.parametrize("kind", ["causal", "none", "full"])
+def test_predictor_first_step_two_queries_with_mask(pkg, device, monkeypatch, kind):
+    """Code predictor step 0: two tokens, a PredictorCache writing positions [0, 2).  The 2x2
+    causal 0/finfo.min mask (continuous.py:39-40) and no mask (two queries attend causally,
+    npu_attention.py:17-18) take the fused two-token launch; any other mask (here all zeros:
+    both queries see both keys) takes the unfused path with the mask applied as given."""
+    import qwen3_tts_engine_amd.packed_attention as packed
+    fused_calls = []
+    original = packed.decode_step
+    monkeypatch.setattr(packed, "decode_step", lambda *a, **k: fused_calls.append(1) or original(*a, **k))
     batch, hidden_size = 12, 256
     model = _Model(Qwen3TTSAttention, 1, hidden_size).to(device).eval()
     pkg.install_packed_attention(model, native_gqa=True)
@@ -158,15 +165,19 @@ def test_predictor_first_step_two_queries_with_mask(pkg, device):
     pos = torch.arange(2, device=device)
     cos, sin = pkg.rope_tables(pos[None].expand(batch, 2).contiguous(), D)
     mask = torch.zeros(1, 1, 2, 2, device=device, dtype=torch.bfloat16)
-    mask[..., 0, 1] = torch.finfo(torch.bfloat16).min
+    if kind == "causal":
+        mask[..., 0, 1] = torch.finfo(torch.bfloat16).min
     q, k, v = _projected(module, hidden)
-    out, _ = module(hidden, (cos, sin), mask, past_key_values=cache, cache_position=pos)
+    out, _ = module(hidden, (cos, sin), None if kind == "none" else mask, past_key_values=cache,
+                    cache_position=pos)
     torch.cuda.synchronize()
+    assert len(fused_calls) == (0 if kind == "full" else 1)
     cb, sb = bits(cos)[:, :, None, :], bits(sin)[:, :, None, :]
     q_rot = obf16.from_bits(orope.rope_bf16(bits(q), cb, sb))
     k_rot = orope.rope_bf16(bits(k), cb, sb).transpose(0, 2, 1, 3)
     assert np.array_equal(bits(cache.keys[0][:, :, :2]), k_rot)
-    m = np.broadcast_to(mask.float().cpu().numpy()[:, 0], (batch, 2, 2))
+    assert np.array_equal(bits(cache.values[0][:, :, :2]), bits(v).transpose(0, 2, 1, 3))
+    m = None if kind == "none" else np.broadcast_to(mask.float().cpu().numpy()[:, 0], (batch, 2, 2))
     expected = oatt.decode_attention(q_rot, obf16.from_bits(k_rot), f64v(v), [1] * batch, D ** -0.5, mask=m)
     assert_attention_close(out.detach().float().cpu().numpy().reshape(batch, 2, HQ, D), expected)
 
