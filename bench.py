@@ -159,9 +159,10 @@ def read_traffic():
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(seconds: float, threads: int = 0):
-    """The reference's torch decode layer (scatter_ write, eager bf16 RoPE, SDPA under the
-    0/finfo.min context mask) on this host, one layer of the same 64-request workload."""
+def cpu_baseline(seconds: float, threads: int = 0, dtype=torch.bfloat16):
+    """The reference's torch decode layer (scatter_ write, eager RoPE, SDPA under the
+    0/finfo.min context mask) on this host, one layer of the same 64-request workload, in
+    bf16 (the GPU path's arithmetic type) or fp32."""
     from oracle import torch_path
 
     previous = torch.get_num_threads()
@@ -170,15 +171,15 @@ def cpu_baseline(seconds: float, threads: int = 0):
     threads = torch.get_num_threads()
     gen = torch.Generator().manual_seed(0)
     contexts = torch.randint(64, 1025, (BATCH,), generator=gen)
-    arena_k = torch.randn(BATCH, HKV, CAPACITY, D, generator=gen).bfloat16()
-    arena_v = torch.randn(BATCH, HKV, CAPACITY, D, generator=gen).bfloat16()
-    qkv = torch.randn(BATCH, 1, (HQ + 2 * HKV) * D, generator=gen).bfloat16()
+    arena_k = torch.randn(BATCH, HKV, CAPACITY, D, generator=gen).to(dtype)
+    arena_v = torch.randn(BATCH, HKV, CAPACITY, D, generator=gen).to(dtype)
+    qkv = torch.randn(BATCH, 1, (HQ + 2 * HKV) * D, generator=gen).to(dtype)
     q = qkv[..., :HQ * D].view(BATCH, 1, HQ, D)
     k = qkv[..., HQ * D:(HQ + HKV) * D].view(BATCH, 1, HKV, D)
     v = qkv[..., (HQ + HKV) * D:].view(BATCH, 1, HKV, D)
     angle = (contexts.float()[:, None] * (1.0 / (1e6 ** (torch.arange(0, D, 2).float() / D)))[None])
     emb = torch.cat([angle, angle], -1)
-    cos, sin = emb.cos().bfloat16()[:, None], emb.sin().bfloat16()[:, None]
+    cos, sin = emb.cos().to(dtype)[:, None], emb.sin().to(dtype)[:, None]
     times = []
     deadline = time.perf_counter() + seconds
     with torch.inference_mode():
@@ -195,7 +196,7 @@ def cpu_baseline(seconds: float, threads: int = 0):
     return {"value": BATCH / (LAYERS * layer_s), "unit": "tokens/s", "cores": threads,
             "kind": "port",
             "sample": (f"median of {len(times)} runs of one talker layer (64 requests, capacity "
-                       f"{CAPACITY}, bf16, torch {threads} threads, {len(os.sched_getaffinity(0))} "
+                       f"{CAPACITY}, {str(dtype).split('.')[-1]}, torch {threads} threads, {len(os.sched_getaffinity(0))} "
                        f"cores in the affinity mask) = {layer_s * 1e3:.2f} ms, scaled to a 28-layer step")}
 
 
@@ -409,6 +410,8 @@ def main():
         # the reference pins torch to 4 threads (model.py:16); reported beside the all-core figure
         four = cpu_baseline(args.cpu_seconds / 2, threads=4)
         result["detail"]["cpu_baseline_4_threads"] = {"value": four["value"], "sample": four["sample"]}
+        fp32 = cpu_baseline(args.cpu_seconds / 2, dtype=torch.float32)
+        result["detail"]["cpu_baseline_fp32"] = {"value": fp32["value"], "sample": fp32["sample"]}
     print(json.dumps(result), flush=True)
 
 
