@@ -79,8 +79,10 @@ __global__ void __launch_bounds__(256) prefill_rope_write_kernel(PrefillRopeWrit
 
 // ---- varlen causal attention on bf16 MFMA tiles ------------------------------------------
 //
-// One workgroup per (request, 64-query block, GH query heads of one KV head), 4 waves per
-// query head; wave w of a head owns queries q0 + 16w ... q0 + 16w + 15.  Keys stream through
+// One workgroup of 4 waves per (request, 64-query block, GH query heads of one KV head);
+// wave w owns queries q0 + 16w ... q0 + 16w + 15 of every one of the GH heads, so each K and
+// V read from LDS feeds the products of all GH heads (GH = 2: 168 VGPRs, 3 waves per SIMD,
+// every workgroup of the 16-prompt workload resident at once).  Keys stream through
 // a ring of kStages LDS stages of kTile keys (K rows then V rows), filled by buffer loads
 // that write LDS directly (16 bytes per lane) kStages - 1 tiles ahead of the products, so
 // the K/V reads never pass through registers.  Rows are stored unpadded with their 16-byte
@@ -96,7 +98,7 @@ __global__ void __launch_bounds__(256) prefill_rope_write_kernel(PrefillRopeWrit
 //                                    ds_read_b64_tr_b16: within a 16-lane group, lane c reads
 //                                    4 dims of key row 4g + c/4 and receives, after the
 //                                    transpose, keys 4g..4g+3 of dim c.
-// Each lane keeps the online-softmax state of one query.  The causal mask is applied only
+// Each lane keeps the online-softmax state of one query per head.  The causal mask is applied only
 // on the steps that straddle the wave's diagonal or the end of the keys.  The running
 // maximum moves only when a step's maximum exceeds it by more than kRescaleLog2 (log2
 // units), so the accumulators are rescaled rarely and unnormalised weights stay below
@@ -163,9 +165,9 @@ Q3T_DEVICE void wait_loads() { asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "m
 Q3T_DEVICE void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 template <int D, int GH>
-__global__ void __launch_bounds__(256 * GH) __attribute__((amdgpu_waves_per_eu(4)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GH == 1 ? 4 : 3)))
 prefill_attention_kernel(PrefillParams p) {
-    constexpr int NT = 256 * GH;                  // threads
+    constexpr int NT = 256;                       // threads
     constexpr int KK = D / 32;                    // MFMA steps over the head dimension
     constexpr int DB = D / 16;                    // 16-row blocks of O^T
     constexpr int CPR = D / 8;                    // 16-byte chunks per row
@@ -182,8 +184,8 @@ prefill_attention_kernel(PrefillParams p) {
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, c = lane & 15;
     const int hgroups = p.Hq / GH;
-    const int hq = (blockIdx.x % hgroups) * GH + wave / 4;  // this wave's query head
-    const int h = hq / p.group;                              // the workgroup's KV head
+    const int hq0 = (blockIdx.x % hgroups) * GH;  // the workgroup's first query head
+    const int h = hq0 / p.group;                 // the workgroup's KV head
     const int rest = blockIdx.x / hgroups;
     // Work item `rest` of this head group: a (64-query block qb, request b) pair, numbered with
     // the longest blocks first.  Up to 64 requests the numbering is dense: only pairs with
@@ -232,7 +234,7 @@ prefill_attention_kernel(PrefillParams p) {
     const int kv_end = (int)min((int64_t)min(n, q0 + kQBlock), p.cap);
     const int ntiles = (kv_end + kTile - 1) / kTile;
     const int64_t slot = p.slots ? p.slots[b] : b;
-    const int wq0 = q0 + 16 * (wave & 3);        // first query of this wave
+    const int wq0 = q0 + 16 * wave;              // first query of this wave
     const int wave_end = min(wq0 + 16, kv_end);  // keys [0, wave_end) can be visible to the wave
     const int mask_from = min(wq0 + 1, kv_end);  // steps reaching past this key need the mask
     const int qpos = wq0 + c;
@@ -291,80 +293,94 @@ prefill_attention_kernel(PrefillParams p) {
         if (s < ntiles) issue(s, s);
 
     // the wave's query rows as B operands: Q[query c][8g + 32kk ...], zeros past the request
-    bf16x8_t qB[KK];
-    {
-        const char *row = p.q + ((int64_t)(t0 + (qvalid ? qpos : 0)) * p.q_st + hq * p.q_sh) * 2;
+    bf16x8_t qB[GH][KK];
+#pragma unroll
+    for (int j = 0; j < GH; ++j) {
+        const char *row = p.q + ((int64_t)(t0 + (qvalid ? qpos : 0)) * p.q_st + (hq0 + j) * p.q_sh) * 2;
         U4 qv[KK];
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) qv[kk] = load16(row + (32 * kk + 8 * g) * 2);
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
             if (!qvalid) qv[kk] = U4{0u, 0u, 0u, 0u};
-            qB[kk] = as_bf16x8(qv[kk]);
+            qB[j][kk] = as_bf16x8(qv[kk]);
         }
     }
 
-    f32x4_t acc[DB];
+    f32x4_t acc[GH][DB];
+    float m[GH], l[GH];  // running maximum (scaled log2 units) and this lane's weight sum
 #pragma unroll
-    for (int db = 0; db < DB; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    float m = 0.f, l = 0.f;  // running maximum (scaled log2 units) and this lane's weight sum
+    for (int j = 0; j < GH; ++j) {
+        m[j] = 0.f;
+        l[j] = 0.f;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) acc[j][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
     bool first = true;
     const float sl = p.scale_log2;
 
     auto step = [&](int kt, uint32_t sbase) {
         const int kb0 = kt * kTile;  // first key of the step
         if (kb0 >= wave_end) return;  // past this wave's keys
-        // S^T for keys kb0 + 16kb + (4g..4g+3)
-        f32x4_t st0 = {0.f, 0.f, 0.f, 0.f}, st1 = {0.f, 0.f, 0.f, 0.f};
-        __builtin_amdgcn_s_setprio(1);  // a wave issuing products goes first, others do the softmax
+        const bool masked = kb0 + kTile > mask_from;  // the step reaches past the diagonal or the keys
+        const int rel = lim - kb0;
+        bf16x8_t pB[GH];
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-            const bf16x8_t a0 = as_bf16x8(lds_read16(sbase + ka[kk]));
-            const bf16x8_t a1 = as_bf16x8(lds_read16(sbase + ka[kk] + 16 * ROW));
-            st0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qB[kk], st0, 0, 0, 0);
-            st1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qB[kk], st1, 0, 0, 0);
-        }
-        __builtin_amdgcn_s_setprio(0);
-        float x[8] = {st0[0], st0[1], st0[2], st0[3], st1[0], st1[1], st1[2], st1[3]};
-        if (kb0 + kTile > mask_from) {  // the step reaches past the diagonal or the keys
-            const int rel = lim - kb0;
+        for (int j = 0; j < GH; ++j) {
+            // S^T of head j for keys kb0 + 16kb + (4g..4g+3); a wave issuing products goes
+            // first, the others do their softmax meanwhile
+            f32x4_t st0 = {0.f, 0.f, 0.f, 0.f}, st1 = {0.f, 0.f, 0.f, 0.f};
+            __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (4 * g + i > rel) x[i] = -INFINITY;
-                if (16 + 4 * g + i > rel) x[4 + i] = -INFINITY;
+            for (int kk = 0; kk < KK; ++kk) {
+                const bf16x8_t a0 = as_bf16x8(lds_read16(sbase + ka[kk]));
+                const bf16x8_t a1 = as_bf16x8(lds_read16(sbase + ka[kk] + 16 * ROW));
+                st0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qB[j][kk], st0, 0, 0, 0);
+                st1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qB[j][kk], st1, 0, 0, 0);
             }
+            __builtin_amdgcn_s_setprio(0);
+            float x[8] = {st0[0], st0[1], st0[2], st0[3], st1[0], st1[1], st1[2], st1[3]};
+            if (masked) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (4 * g + i > rel) x[i] = -INFINITY;
+                    if (16 + 4 * g + i > rel) x[4 + i] = -INFINITY;
+                }
+            }
+            float mx = x[0];
+#pragma unroll
+            for (int e = 1; e < 8; ++e) mx = __builtin_amdgcn_fmed3f(mx, x[e], __builtin_inff());
+            mx = __builtin_amdgcn_fmed3f(mx, xor16(mx), __builtin_inff());
+            mx = __builtin_amdgcn_fmed3f(mx, xor32(mx), __builtin_inff());
+            const float mt = mx * sl;
+            if (first) {
+                m[j] = mt;
+            } else if (__builtin_amdgcn_ballot_w64(mt > m[j] + kRescaleLog2) != 0) {
+                const float mn = fmaxf(m[j], mt);
+                const float alpha = fexp2(m[j] - mn);
+                m[j] = mn;
+                l[j] *= alpha;
+#pragma unroll
+                for (int db = 0; db < DB; ++db) acc[j][db] *= alpha;
+            }
+            float pv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) pv[e] = fexp2(__builtin_fmaf(x[e], sl, -m[j]));
+            l[j] += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+            const U4 packed = {cvt_pk_bf16(pv[0], pv[1]), cvt_pk_bf16(pv[2], pv[3]),
+                               cvt_pk_bf16(pv[4], pv[5]), cvt_pk_bf16(pv[6], pv[7])};
+            pB[j] = as_bf16x8(packed);
         }
-        float mx = x[0];
-#pragma unroll
-        for (int e = 1; e < 8; ++e) mx = __builtin_amdgcn_fmed3f(mx, x[e], __builtin_inff());
-        mx = __builtin_amdgcn_fmed3f(mx, xor16(mx), __builtin_inff());
-        mx = __builtin_amdgcn_fmed3f(mx, xor32(mx), __builtin_inff());
-        const float mt = mx * sl;
-        if (first) {
-            m = mt;
-            first = false;
-        } else if (__builtin_amdgcn_ballot_w64(mt > m + kRescaleLog2) != 0) {
-            const float mn = fmaxf(m, mt);
-            const float alpha = fexp2(m - mn);
-            m = mn;
-            l *= alpha;
-#pragma unroll
-            for (int db = 0; db < DB; ++db) acc[db] *= alpha;
-        }
-        float pv[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pv[e] = fexp2(__builtin_fmaf(x[e], sl, -m));
-        l += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
-        const U4 packed = {cvt_pk_bf16(pv[0], pv[1]), cvt_pk_bf16(pv[2], pv[3]),
-                           cvt_pk_bf16(pv[4], pv[5]), cvt_pk_bf16(pv[6], pv[7])};
-        const bf16x8_t pB = as_bf16x8(packed);
-        // O^T += V^T . P^T
+        first = false;
+        // O^T += V^T . P^T, one V read for every head
         __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
             const uint2 lo = lds_read_tr16(sbase + va[db]), hi = lds_read_tr16(sbase + va[db] + 16 * ROW);
-            const bf16x8_t a = as_bf16x8(U4{lo.x, lo.y, hi.x, hi.y});
-            acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pB, acc[db], 0, 0, 0);
+            const bf16x8_t av = as_bf16x8(U4{lo.x, lo.y, hi.x, hi.y});
+#pragma unroll
+            for (int j = 0; j < GH; ++j)
+                acc[j][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pB[j], acc[j][db], 0, 0, 0);
         }
         __builtin_amdgcn_s_setprio(0);
     };
@@ -386,15 +402,18 @@ prefill_attention_kernel(PrefillParams p) {
     }
 
     if (!qvalid) return;
-    float lt = l + xor16(l);
-    lt += xor32(lt);
-    const float inv = __builtin_amdgcn_rcpf(lt);
-    char *orow = p.out + ((int64_t)(t0 + qpos) * p.o_st + hq * p.o_sh) * 2;
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-        const uint2 v = {cvt_pk_bf16(acc[db][0] * inv, acc[db][1] * inv),
-                         cvt_pk_bf16(acc[db][2] * inv, acc[db][3] * inv)};
-        *reinterpret_cast<uint2 *>(orow + (16 * db + 4 * g) * 2) = v;
+    for (int j = 0; j < GH; ++j) {
+        float lt = l[j] + xor16(l[j]);
+        lt += xor32(lt);
+        const float inv = __builtin_amdgcn_rcpf(lt);
+        char *orow = p.out + ((int64_t)(t0 + qpos) * p.o_st + (hq0 + j) * p.o_sh) * 2;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            const uint2 v = {cvt_pk_bf16(acc[j][db][0] * inv, acc[j][db][1] * inv),
+                             cvt_pk_bf16(acc[j][db][2] * inv, acc[j][db][3] * inv)};
+            *reinterpret_cast<uint2 *>(orow + (16 * db + 4 * g) * 2) = v;
+        }
     }
 }
 
@@ -443,7 +462,7 @@ extern "C" int q3t_prefill_rope_write(const q3t_prefill_rope_write_args *a, void
 template <int D, int GH>
 static void launch_prefill(const PrefillParams &p, hipStream_t s) {
     hipLaunchKernelGGL((prefill_attention_kernel<D, GH>), dim3((uint32_t)p.B * p.nqb * (p.Hq / GH)),
-                       dim3(256 * GH), 0, s, p);
+                       dim3(256), 0, s, p);
 }
 
 extern "C" int q3t_prefill_attention(const q3t_prefill_args *a, void *stream) {
