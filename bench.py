@@ -67,17 +67,17 @@ def prefill_detail(pkg, device, reps=20):
     cos, sin = pkg.rope_tables(positions, D)
     dcu = cu.to(device)
     out = torch.empty(LAYERS, total, HQ, D, device=device, dtype=torch.bfloat16)
-    q_rot = torch.empty(LAYERS, total, HQ, D, device=device, dtype=torch.bfloat16)
 
     def step(attention_only):
+        # prefill_step's kernels: the K/V prologue, then attention rotating the raw queries
         for layer in range(LAYERS):
             row = qkv[layer]
             q, k, v = row[:, :HQ], row[:, HQ:HQ + HKV], row[:, HQ + HKV:]
             if not attention_only:
                 pkg.prefill_rope_write(q, k, v, cos, sin, dcu, arena[layer], arena[LAYERS + layer],
-                                       q_out=q_rot[layer])
-            pkg.prefill_attention(q_rot[layer], arena[layer], arena[LAYERS + layer], dcu, longest,
-                                  out=out[layer])
+                                       rotate_query=False)
+            pkg.prefill_attention(q, arena[layer], arena[LAYERS + layer], dcu, longest,
+                                  out=out[layer], cos=cos, sin=sin)
 
     times = {}
     for attention_only in (False, True):

@@ -209,6 +209,12 @@ typedef struct q3t_prefill_args {
     void *out;                     /* (tokens, q_heads, head_dim) bf16 */
     int64_t o_stride_t, o_stride_h;
     int64_t capacity;              /* key rows per slot in the arena views */
+    /* optional bf16 cos/sin rows (tokens, head_dim) of each query token's position: the
+       query rows are then un-rotated and RoPE (bf16-exact, as q3t_rotary) is applied as
+       they are loaded, so no rotated copy of the queries is written; NULL = the query rows
+       are already rotated */
+    const void *cos, *sin;
+    int64_t cs_stride_t;
 } q3t_prefill_args;
 
 int q3t_prefill_attention(const q3t_prefill_args *args, void *stream);
@@ -216,7 +222,9 @@ int q3t_prefill_attention(const q3t_prefill_args *args, void *stream);
 /*
  * Prefill prologue: RoPE of packed query/key rows at positions 0 ... len_b - 1 (cos/sin
  * rows indexed by token) and the paired write of rotated keys and raw values into the
- * arena slot of each request.  q_out receives the rotated queries.
+ * arena slot of each request.  q_out receives the rotated queries; with q_out == NULL only
+ * the keys and values are handled (query and its strides are then ignored) and
+ * q3t_prefill_attention rotates the queries itself from its cos/sin arguments.
  * Replaces: the per-layer RoPE + DynamicCache fill of PrefillGraph.compute
  * (prefill_graph.py:38-43) and the later copy_packed_prefix into the arena
  * (continuous.py:468-469).

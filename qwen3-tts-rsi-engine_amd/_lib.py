@@ -62,6 +62,7 @@ class PrefillArgs(ctypes.Structure):
         ("v_stride_b", c_i64), ("v_stride_h", c_i64), ("v_stride_t", c_i64),
         ("kv_slots", c_vp), ("out", c_vp), ("o_stride_t", c_i64), ("o_stride_h", c_i64),
         ("capacity", c_i64),
+        ("cos", c_vp), ("sin", c_vp), ("cs_stride_t", c_i64),
     ]
 
 
@@ -107,7 +108,7 @@ class KernelError(RuntimeError):
     """A HIP launch failed after host validation passed."""
 
 
-ABI_VERSION = 2  # q3t_abi_version() of the header these structures mirror
+ABI_VERSION = 3  # q3t_abi_version() of the header these structures mirror
 
 
 def library() -> ctypes.CDLL:

@@ -257,10 +257,12 @@ def attention(module, query, key, value, attention_mask, **kwargs):
 
 
 def prefill_attention(query, keys, values, cu_seqlens, max_seqlen, *, scale=None, kv_slots=None,
-                      out=None):
+                      out=None, cos=None, sin=None):
     """Varlen causal GQA: query (T, Hq, D) packed by cu_seqlens (B+1, int32); keys/values
     (slots, Hkv, capacity, D) arena views holding each request's keys at positions
-    0 ... len-1 (slot b, or kv_slots[b]).  Returns (T, Hq, D)."""
+    0 ... len-1 (slot b, or kv_slots[b]).  Returns (T, Hq, D).  With cos/sin (bf16 (T, D)
+    rows of each token's position) the query rows are un-rotated and the kernel applies
+    RoPE as it loads them (bf16-exact, as ``rotary``)."""
     if query.ndim != 3 or keys.ndim != 4 or values.shape != keys.shape:
         raise ValueError('expected (T, Hq, D) queries and arena key/value views')
     total, q_heads, head_dim = query.shape
@@ -294,6 +296,14 @@ def prefill_attention(query, keys, values, cu_seqlens, max_seqlen, *, scale=None
     a.out = out.data_ptr()
     a.o_stride_t, a.o_stride_h = out.stride()[:2]
     a.capacity = keys.shape[2]
+    if (cos is None) != (sin is None):
+        raise ValueError('cos and sin come together')
+    if cos is not None:
+        if (cos.shape != (total, head_dim) or sin.shape != cos.shape or cos.dtype != torch.bfloat16
+                or sin.dtype != torch.bfloat16 or cos.stride(1) != 1 or sin.stride() != cos.stride()):
+            raise ValueError('cos/sin must be bf16 (tokens, head_dim) rows')
+        _lib.require_gpu(query, cos, sin)
+        a.cos, a.sin, a.cs_stride_t = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
     status = _lib.library().q3t_prefill_attention(a, _lib.stream_handle(device))
     _lib.check(status, 'prefill attention')
     return out

@@ -34,11 +34,13 @@ Q3T_DEVICE int request_of(const int32_t *cu, int B, int64_t t) {
 }
 
 // One work item: 8 dims of each half of one (token, head) row.  Heads [0, Hq) are query
-// heads (rotated into q_out); heads [Hq, Hq+Hkv) rotate the key and copy the value into
-// the arena at the token's position within its request.
+// heads (rotated into q_out; absent when q_out is null, the attention kernel then rotates
+// the queries itself); the Hkv heads after them rotate the key and copy the value into the
+// arena at the token's position within its request.
 __global__ void __launch_bounds__(256) prefill_rope_write_kernel(PrefillRopeWriteParams p) {
     const int vecs = p.D / 16;
-    const int heads = p.Hq + p.Hkv;
+    const int qh = p.qo ? p.Hq : 0;  // without q_out only the key/value rows are handled
+    const int heads = qh + p.Hkv;
     const int64_t total = p.T * heads * vecs;
     const int half = p.D / 2;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
@@ -50,7 +52,7 @@ __global__ void __launch_bounds__(256) prefill_rope_write_kernel(PrefillRopeWrit
         const char *crow = p.cs + t * p.cs_st * 2, *srow = p.sn + t * p.cs_st * 2;
         U4 c1 = load16(crow + c * 16), c2 = load16(crow + (half + c * 8) * 2);
         U4 s1 = load16(srow + c * 16), s2 = load16(srow + (half + c * 8) * 2);
-        if (hd < p.Hq) {
+        if (hd < qh) {
             const char *row = p.q + (t * p.q_st + hd * p.q_sh) * 2;
             U4 x1 = load16(row + c * 16), x2 = load16(row + (half + c * 8) * 2), y1, y2;
             rope8(&x1.x, &x2.x, &c1.x, &c2.x, &s1.x, &s2.x, &y1.x, &y2.x);
@@ -58,7 +60,7 @@ __global__ void __launch_bounds__(256) prefill_rope_write_kernel(PrefillRopeWrit
             store16(orow + c * 16, y1);
             store16(orow + (half + c * 8) * 2, y2);
         } else {
-            const int h = hd - p.Hq;
+            const int h = hd - qh;
             const int b = request_of(p.cu, p.B, t);
             const int64_t pos = t - p.cu[b];
             if (pos < 0 || pos >= p.capacity) continue;
@@ -126,6 +128,8 @@ struct PrefillParams {
     const int64_t *slots;
     char *out;
     int64_t o_st, o_sh;
+    const char *cs, *sn;  // optional cos/sin rows per token: the query rows are rotated on load
+    int64_t cs_st;
 };
 
 Q3T_DEVICE bf16x8_t as_bf16x8(const U4 &v) { return __builtin_bit_cast(bf16x8_t, v); }
@@ -294,12 +298,39 @@ prefill_attention_kernel(PrefillParams p) {
 
     // the wave's query rows as B operands: Q[query c][8g + 32kk ...], zeros past the request
     bf16x8_t qB[GH][KK];
+    // with cos/sin: the lane's RoPE rows (its query token, dims 32kk + 8g ... + 7 and the same
+    // dims D/2 further), shared by the GH heads
+    U4 rc1[KK / 2], rc2[KK / 2], rs1[KK / 2], rs2[KK / 2];
+    if (p.cs) {
+        const int64_t tr = (int64_t)(t0 + (qvalid ? qpos : 0)) * p.cs_st * 2;
+#pragma unroll
+        for (int kk = 0; kk < KK / 2; ++kk) {
+            const int d1 = (32 * kk + 8 * g) * 2, d2 = d1 + D;  // bytes of dims d and d + D/2
+            rc1[kk] = load16(p.cs + tr + d1);
+            rc2[kk] = load16(p.cs + tr + d2);
+            rs1[kk] = load16(p.sn + tr + d1);
+            rs2[kk] = load16(p.sn + tr + d2);
+        }
+    }
 #pragma unroll
     for (int j = 0; j < GH; ++j) {
         const char *row = p.q + ((int64_t)(t0 + (qvalid ? qpos : 0)) * p.q_st + (hq0 + j) * p.q_sh) * 2;
         U4 qv[KK];
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) qv[kk] = load16(row + (32 * kk + 8 * g) * 2);
+        if (p.cs) {
+            // rotate-half RoPE in registers (bf16-exact; the rotated rows are never stored, so
+            // NaN payloads need no canonical form): the lane's dims 32kk + 8g ... + 7 pair with
+            // the same dims of kk + KK/2, which the lane holds as well
+#pragma unroll
+            for (int kk = 0; kk < KK / 2; ++kk) {
+                U4 y1, y2;
+                rope8<false>(&qv[kk].x, &qv[kk + KK / 2].x, &rc1[kk].x, &rc2[kk].x, &rs1[kk].x, &rs2[kk].x,
+                             &y1.x, &y2.x);
+                qv[kk] = y1;
+                qv[kk + KK / 2] = y2;
+            }
+        }
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
             if (!qvalid) qv[kk] = U4{0u, 0u, 0u, 0u};
@@ -428,15 +459,18 @@ extern "C" int q3t_prefill_rope_write(const q3t_prefill_rope_write_args *a, void
         return Q3T_EINVAL;
     if (a->head_dim != 64 && a->head_dim != 128) return Q3T_EUNSUPPORTED;
     if (a->total_tokens == 0) return Q3T_OK;
-    if (!a->cu_seqlens || !a->query || !a->key || !a->value || !a->cos || !a->sin || !a->q_out ||
+    // q_out == NULL: keys and values only (the attention kernel rotates the queries itself)
+    const bool with_q = a->q_out != nullptr;
+    if (!a->cu_seqlens || (with_q && !a->query) || !a->key || !a->value || !a->cos || !a->sin ||
         !a->arena_keys || !a->arena_values)
         return Q3T_EINVAL;
-    const int64_t st[] = {a->q_stride_t, a->q_stride_h, a->k_stride_t, a->k_stride_h,
-                          a->v_stride_t, a->v_stride_h, a->cs_stride_t, a->qo_stride_t,
-                          a->qo_stride_h, a->a_stride_b, a->a_stride_h, a->a_stride_t};
+    const int64_t st[] = {with_q ? a->q_stride_t : 0, with_q ? a->q_stride_h : 0, a->k_stride_t, a->k_stride_h,
+                          a->v_stride_t, a->v_stride_h, a->cs_stride_t, with_q ? a->qo_stride_t : 0,
+                          with_q ? a->qo_stride_h : 0, a->a_stride_b, a->a_stride_h, a->a_stride_t};
     for (int64_t s : st)
         if ((s * 2) % 16) return Q3T_EINVAL;
-    const void *ptrs[] = {a->query, a->key, a->value, a->cos, a->sin, a->q_out, a->arena_keys, a->arena_values};
+    const void *ptrs[] = {with_q ? a->query : a->key, a->key, a->value, a->cos, a->sin,
+                          with_q ? a->q_out : a->key, a->arena_keys, a->arena_values};
     for (const void *q : ptrs)
         if (!aligned(q, 16)) return Q3T_EINVAL;
     PrefillRopeWriteParams p;
@@ -450,7 +484,7 @@ extern "C" int q3t_prefill_rope_write(const q3t_prefill_rope_write_args *a, void
     p.ak = (char *)a->arena_keys; p.av = (char *)a->arena_values;
     p.a_sb = a->a_stride_b; p.a_sh = a->a_stride_h; p.a_st = a->a_stride_t;
     p.slots = a->kv_slots;
-    const int64_t total = p.T * (p.Hq + p.Hkv) * (p.D / 16);
+    const int64_t total = p.T * ((with_q ? p.Hq : 0) + p.Hkv) * (p.D / 16);
     int64_t blocks = (total + 255) / 256;
     if (blocks > 16384) blocks = 16384;
     hipLaunchKernelGGL(prefill_rope_write_kernel, dim3((unsigned)blocks), dim3(256), 0,
@@ -482,6 +516,9 @@ extern "C" int q3t_prefill_attention(const q3t_prefill_args *a, void *stream) {
         if (v < 0 || (v * 2) % 16) return Q3T_EINVAL;
     if (!aligned(a->query, 16) || !aligned(a->keys, 16) || !aligned(a->values, 16) || !aligned(a->out, 8))
         return Q3T_EINVAL;
+    if ((a->cos != nullptr) != (a->sin != nullptr)) return Q3T_EINVAL;
+    if (a->cos && (!aligned(a->cos, 16) || !aligned(a->sin, 16) || a->cs_stride_t < 0 || (a->cs_stride_t * 2) % 16))
+        return Q3T_EINVAL;
     // key rows of one (slot, head) are addressed by 32-bit byte offsets
     const int64_t max_st = a->k_stride_t > a->v_stride_t ? a->k_stride_t : a->v_stride_t;
     if (a->capacity * max_st * 2 + a->head_dim * 2 > INT32_MAX) return Q3T_EUNSUPPORTED;
@@ -500,6 +537,7 @@ extern "C" int q3t_prefill_attention(const q3t_prefill_args *a, void *stream) {
     p.cap = a->capacity;
     p.T = a->total_tokens;
     p.out = (char *)a->out; p.o_st = a->o_stride_t; p.o_sh = a->o_stride_h;
+    p.cs = (const char *)a->cos; p.sn = (const char *)a->sin; p.cs_st = a->cs_stride_t;
     hipStream_t s = (hipStream_t)stream;
     // the query heads of a KV head pair up in one workgroup and share its staged K/V tiles
     if (G % 2 == 0) {

@@ -128,23 +128,29 @@ Q3T_DEVICE void store16(void *p, U4 v) { *reinterpret_cast<U4 *>(p) = v; }
 //   y1 = bf16(bf16(x1*c1) + bf16(-x2*s1)),  y2 = bf16(bf16(x2*c2) + bf16(x1*s2)).
 // Products of two bf16 values are exact in fp32; each sum rounds to fp32 and then to bf16,
 // the same double rounding torch performs for a bf16 add.
+// CANON = false leaves NaN payloads as the conversion produces them (for rotated values that
+// are consumed in registers and never stored).
+template <bool CANON = true>
 Q3T_DEVICE void rope_pair(uint32_t x1, uint32_t x2, uint32_t c1, uint32_t c2, uint32_t s1,
                           uint32_t s2, uint32_t &y1, uint32_t &y2) {
     const float a0 = bf16_lo(x1), a1 = bf16_hi(x1), b0 = bf16_lo(x2), b1 = bf16_hi(x2);
     // intermediate roundings: a NaN only has to stay a NaN, its bits are canonicalised at the end
     const uint32_t l1 = cvt_pk_bf16(a0 * bf16_lo(c1), a1 * bf16_hi(c1));
     const uint32_t r1 = cvt_pk_bf16(-(b0 * bf16_lo(s1)), -(b1 * bf16_hi(s1)));
-    y1 = cvt_pk_bf16_canon(bf16_lo(l1) + bf16_lo(r1), bf16_hi(l1) + bf16_hi(r1));
+    y1 = CANON ? cvt_pk_bf16_canon(bf16_lo(l1) + bf16_lo(r1), bf16_hi(l1) + bf16_hi(r1))
+               : cvt_pk_bf16(bf16_lo(l1) + bf16_lo(r1), bf16_hi(l1) + bf16_hi(r1));
     const uint32_t l2 = cvt_pk_bf16(b0 * bf16_lo(c2), b1 * bf16_hi(c2));
     const uint32_t r2 = cvt_pk_bf16(a0 * bf16_lo(s2), a1 * bf16_hi(s2));
-    y2 = cvt_pk_bf16_canon(bf16_lo(l2) + bf16_lo(r2), bf16_hi(l2) + bf16_hi(r2));
+    y2 = CANON ? cvt_pk_bf16_canon(bf16_lo(l2) + bf16_lo(r2), bf16_hi(l2) + bf16_hi(r2))
+               : cvt_pk_bf16(bf16_lo(l2) + bf16_lo(r2), bf16_hi(l2) + bf16_hi(r2));
 }
 
 // RoPE on 8 consecutive dims of each half (one 16-byte vector per half).
+template <bool CANON = true>
 Q3T_DEVICE void rope8(const uint32_t *x1, const uint32_t *x2, const uint32_t *c1, const uint32_t *c2,
                       const uint32_t *s1, const uint32_t *s2, uint32_t *y1, uint32_t *y2) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) rope_pair(x1[i], x2[i], c1[i], c2[i], s1[i], s2[i], y1[i], y2[i]);
+    for (int i = 0; i < 4; ++i) rope_pair<CANON>(x1[i], x2[i], c1[i], c2[i], s1[i], s2[i], y1[i], y2[i]);
 }
 
 // RoPE of one 16-byte vector (8 dims) of a row, as rope_pair computes it: `own` holds the

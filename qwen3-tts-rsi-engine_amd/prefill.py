@@ -9,10 +9,12 @@ into the arena slots, and the attention reads them from there:
 
 * ``prefill_rope_write`` - RoPE of query and key rows at positions 0 ... len-1 of each
   request (bf16-exact, as ``rotary``) and the paired K/V write into the arena
-  (kernel ``q3t_prefill_rope_write``);
+  (kernel ``q3t_prefill_rope_write``); with ``rotate_query=False`` the keys and values only;
 * ``prefill_attention`` - varlen causal GQA on bf16 MFMA tiles (kernel
-  ``q3t_prefill_attention``, re-exported from ``attention``);
-* ``prefill_step`` - both, for one layer.
+  ``q3t_prefill_attention``, re-exported from ``attention``); given cos/sin it rotates the
+  raw query rows as it loads them;
+* ``prefill_step`` - one layer: the K/V prologue, then attention over the raw queries with
+  their RoPE applied in the attention kernel (no rotated copy of the queries is written).
 """
 import torch
 
@@ -28,11 +30,12 @@ def _check_packed(name, t, tokens, heads, width):
 
 
 def prefill_rope_write(query, key, value, cos, sin, cu_seqlens, key_arena, value_arena, *,
-                       kv_slots=None, q_out=None):
+                       kv_slots=None, q_out=None, rotate_query=True):
     """query (T, Hq, D), key/value (T, Hkv, D) packed by cu_seqlens (B+1, int32 device);
     cos/sin (T, D) rows of each token's position; arena planes (slots, Hkv, C, D).
     Writes rotated keys and values at positions 0 ... len_b-1 of slot b (or kv_slots[b])
-    and returns the rotated queries (T, Hq, D)."""
+    and returns the rotated queries (T, Hq, D), or None with ``rotate_query=False`` (the
+    query rows are then not touched)."""
     if query.ndim != 3 or key.ndim != 3:
         raise ValueError('expected packed (tokens, heads, head_dim) rows')
     tokens, q_heads, head_dim = query.shape
@@ -57,7 +60,10 @@ def prefill_rope_write(query, key, value, cos, sin, cu_seqlens, key_arena, value
         raise ValueError('the arena has fewer slots than requests')
     device = _lib.require_gpu(query, key, value, cos, sin, cu_seqlens, key_arena, value_arena,
                               *([kv_slots] if kv_slots is not None else []))
-    if q_out is None:
+    if not rotate_query:
+        if q_out is not None:
+            raise ValueError('q_out is only written with rotate_query=True')
+    elif q_out is None:
         q_out = torch.empty_like(query, memory_format=torch.contiguous_format)
     else:
         _check_packed('q_out', q_out, tokens, q_heads, head_dim)
@@ -69,7 +75,8 @@ def prefill_rope_write(query, key, value, cos, sin, cu_seqlens, key_arena, value
     a.key, (a.k_stride_t, a.k_stride_h) = key.data_ptr(), key.stride()[:2]
     a.value, (a.v_stride_t, a.v_stride_h) = value.data_ptr(), value.stride()[:2]
     a.cos, a.sin, a.cs_stride_t = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
-    a.q_out, (a.qo_stride_t, a.qo_stride_h) = q_out.data_ptr(), q_out.stride()[:2]
+    if q_out is not None:
+        a.q_out, (a.qo_stride_t, a.qo_stride_h) = q_out.data_ptr(), q_out.stride()[:2]
     a.arena_keys, a.arena_values = key_arena.data_ptr(), value_arena.data_ptr()
     a.a_stride_b, a.a_stride_h, a.a_stride_t = key_arena.stride()[:3]
     if kv_slots is not None:
@@ -83,7 +90,7 @@ def prefill_step(query, key, value, cos, sin, cu_seqlens, max_seqlen, key_arena,
                  kv_slots=None, scale=None, out=None):
     """One prefill layer over packed prompts: RoPE, arena write, causal GQA.
     Returns the attention output (T, Hq, D)."""
-    q_rot = prefill_rope_write(query, key, value, cos, sin, cu_seqlens, key_arena, value_arena,
-                               kv_slots=kv_slots)
-    return prefill_attention(q_rot, key_arena, value_arena, cu_seqlens, max_seqlen, scale=scale,
-                             kv_slots=kv_slots, out=out)
+    prefill_rope_write(query, key, value, cos, sin, cu_seqlens, key_arena, value_arena,
+                       kv_slots=kv_slots, rotate_query=False)
+    return prefill_attention(query, key_arena, value_arena, cu_seqlens, max_seqlen, scale=scale,
+                             kv_slots=kv_slots, out=out, cos=cos, sin=sin)

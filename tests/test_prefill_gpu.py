@@ -69,6 +69,38 @@ def test_prefill_workload_rope_write_and_attention(pkg, device):
 
 @pytest.mark.parametrize("group", [1, 2, 4])
 @pytest.mark.parametrize("head_dim", [64, 128])
+def test_prefill_rotates_queries_in_the_attention_kernel(pkg, device, group, head_dim):
+    """prefill_step: the prologue writes only the keys and values, the attention kernel applies
+    RoPE to the raw query rows as it loads them.  Same bits as the rotated-copy path (the
+    rotation is the same bf16-exact arithmetic), and the query rows are left untouched."""
+    lengths = [1, 15, 16, 17, 64, 65, 200, 333]
+    kv_heads = 2
+    q_heads = kv_heads * group
+    q, k, v, cu, positions = _packed(lengths, q_heads, kv_heads, head_dim, 7 + group)
+    cos_b, sin_b = _tables(positions, head_dim)
+    cos = torch.from_numpy(cos_b.view(np.int16)).view(torch.bfloat16).to(device)
+    sin = torch.from_numpy(sin_b.view(np.int16)).view(torch.bfloat16).to(device)
+    dg = torch.Generator(device=device).manual_seed(8)
+    ak = torch.randn(len(lengths), kv_heads, 384, head_dim, generator=dg, device=device, dtype=torch.bfloat16)
+    av = torch.randn(len(lengths), kv_heads, 384, head_dim, generator=dg, device=device, dtype=torch.bfloat16)
+    ak2, av2 = ak.clone(), av.clone()
+    dq, dk, dv, dcu = q.to(device), k.to(device), v.to(device), cu.to(device)
+    raw = bits(dq).copy()
+    fused = pkg.prefill_step(dq, dk, dv, cos, sin, dcu, max(lengths), ak, av)
+    q_rot = pkg.prefill_rope_write(dq, dk, dv, cos, sin, dcu, ak2, av2)
+    chain = pkg.prefill_attention(q_rot, ak2, av2, dcu, max(lengths))
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(dq), raw)
+    assert torch.equal(ak, ak2) and torch.equal(av, av2)
+    assert torch.equal(fused, chain)
+    eq = orope.rope_bf16(bits(q), cos_b[:, None, :], sin_b[:, None, :])
+    expected = oatt.prefill_attention(obf16.from_bits(eq), obf16.from_bits(bits(ak)), obf16.from_bits(bits(av)),
+                                      cu.numpy(), head_dim ** -0.5)
+    assert_attention_close(f64(fused), expected)
+
+
+@pytest.mark.parametrize("group", [1, 2, 4])
+@pytest.mark.parametrize("head_dim", [64, 128])
 def test_prefill_attention_tile_edges(pkg, device, group, head_dim):
     """Lengths on and around the 32-key and 64-query tile edges, an empty request and a
     single token; max_seqlen above the longest request."""
