@@ -281,7 +281,7 @@ def main():
                              "(for per-kernel profiling of the prefill kernels)")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
+        print("bench.py measures one GPU: the package has no multi-GPU path "
               "(decode would shard by request slot, one arena per GPU)", file=sys.stderr)
         sys.exit(2)
 

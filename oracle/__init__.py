@@ -3,8 +3,8 @@
 A restatement, in numpy (and torch-CPU for the timed baseline), of what the reference
 engine (InferMatrixLab/qwen3-tts-rsi-engine) computes on this path.  Each function cites
 the reference file:line it follows.  Only ``tests/``, ``__graft_entry__.smoke()`` and
-``bench.py``'s CPU-baseline leg may import this package, and only as the checker or the
-timed CPU baseline; the product path (the ``qwen3-tts-rsi-engine_amd`` package) never
+``bench.py``'s CPU-baseline leg may import this package, and only to check results or as
+the timed CPU baseline; the product path (the ``qwen3-tts-rsi-engine_amd`` package) never
 calls it.
 
 How each part is pinned (checked by tests/test_oracle.py, never by retyping a formula):

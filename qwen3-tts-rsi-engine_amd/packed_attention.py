@@ -22,7 +22,7 @@ signature compatibility):
 * and the predictor's first step, two tokens under the 2x2 causal mask (continuous.py:39-40,
   zeros with finfo.min above the diagonal, or no mask, which the attention treats as causal
   for two queries): ``decode_step`` writes positions 0 and 1 and attends them causally.  The
-  mask's values are read once, outside graph capture, and the verdict is kept per mask
+  mask's values are read once, outside graph capture, and the result is kept per mask
   tensor;
 * every other call rotates q/k with ``rotary`` (bf16-exact to torch eager), lets the cache
   update and calls ``attention`` (the npu_attention.attention drop-in).
@@ -64,10 +64,10 @@ def _is_causal_pair(mask, batch):
             return False
         values = mask.detach().float().cpu()
         low = torch.finfo(mask.dtype).min
-        verdict = bool((values[..., 0, 0] == 0).all() and (values[..., 1, 0] == 0).all()
-                       and (values[..., 1, 1] == 0).all() and (values[..., 0, 1] <= low).all())
+        causal = bool((values[..., 0, 0] == 0).all() and (values[..., 1, 0] == 0).all()
+                      and (values[..., 1, 1] == 0).all() and (values[..., 0, 1] <= low).all())
         # the entry keeps the mask alive, so its address cannot be reused by another tensor
-        seen = _CAUSAL_PAIR[key] = (verdict, mask)
+        seen = _CAUSAL_PAIR[key] = (causal, mask)
     return seen[0]
 
 
