@@ -18,6 +18,9 @@ Fixtures:
   config2_talker64.npz   the 64-request ragged talker step (contexts U[64, 1024], seed 0,
                          sum 32,718): digests of the arena after the write and the
                          attention output of 8 of the requests
+  prefill16.npz          the 16-prompt prefill (lengths randint(32, 513), seed 0, 4790
+                         tokens): SHA-256 of the arena after the rotated K/V write and the
+                         attention output of each prompt's last token (prefill_graph.py:31-50)
   scheduler_trace.json   the 128-slot, 200-iteration mixed trace under three scheduler
                          settings: per-iteration decode records and device operations
                          (continuous.py:353-363, 425-473, 541-657)
@@ -90,6 +93,23 @@ def config2_inputs():
     values = torch.randn(64, HKV, 1024, D, generator=gen).bfloat16()
     qkv = torch.randn(64, 1, (HQ + 2 * HKV) * D, generator=gen).bfloat16()
     return contexts, keys, values, qkv
+
+
+PREFILL_SLOTS, PREFILL_CAPACITY = 16, 512
+
+
+def prefill_inputs():
+    """Seed 0: lengths randint(32, 513, (16,)), then q (T, 16, 128), k and v (T, 8, 128),
+    N(0,1) rounded to bf16; request b fills slot b of a zeroed (16, 8, 512, 128) arena."""
+    gen = torch.Generator().manual_seed(0)
+    lengths = torch.randint(32, 513, (16,), generator=gen)
+    total = int(lengths.sum())
+    q = torch.randn(total, HQ, D, generator=gen).bfloat16()
+    k = torch.randn(total, HKV, D, generator=gen).bfloat16()
+    v = torch.randn(total, HKV, D, generator=gen).bfloat16()
+    cu = np.concatenate([[0], np.cumsum(lengths.numpy())]).astype(np.int32)
+    positions = np.concatenate([np.arange(int(n)) for n in lengths])
+    return lengths.numpy(), cu, positions, q, k, v
 
 
 def split_qkv(qkv):
@@ -166,6 +186,30 @@ def expected_config2():
             'q_rot_sha256': np.asarray(sha256(q_rot))}
 
 
+def prefill_tables(positions):
+    """bf16 cos/sin rows of the prefill tokens (the oracle tables, pinned by rope_bf16.npz)."""
+    return orope.tables(positions, orope.inv_freq(D))
+
+
+def expected_prefill():
+    lengths, cu, positions, q, k, v = prefill_inputs()
+    cos, sin = prefill_tables(positions)
+    q_rot = orope.rope_bf16(to_bits(q), cos[:, None, :], sin[:, None, :])
+    k_rot = orope.rope_bf16(to_bits(k), cos[:, None, :], sin[:, None, :])
+    ak = np.zeros((PREFILL_SLOTS, HKV, PREFILL_CAPACITY, D), np.uint16)
+    av = np.zeros_like(ak)
+    vb = to_bits(v)
+    for b, n in enumerate(lengths):
+        t0 = int(cu[b])
+        ak[b, :, :n] = k_rot[t0:t0 + n].transpose(1, 0, 2)
+        av[b, :, :n] = vb[t0:t0 + n].transpose(1, 0, 2)
+    out = oatt.prefill_attention(obf16.from_bits(q_rot), obf16.from_bits(ak), obf16.from_bits(av), cu, D ** -0.5)
+    last = cu[1:] - 1
+    return {'lengths': lengths.astype(np.int64), 'last_tokens': last.astype(np.int64),
+            'out_last': out[last].astype(np.float32),
+            'keys_sha256': np.asarray(sha256(ak)), 'values_sha256': np.asarray(sha256(av))}
+
+
 def expected_scheduler():
     runs = []
     for step, bucket_kv, cancel_rate in SCHEDULER_SETTINGS:
@@ -180,6 +224,7 @@ def main():
     np.savez_compressed(HERE / 'rope_bf16.npz', **expected_rope())
     np.savez_compressed(HERE / 'config1_fp32.npz', **expected_config1())
     np.savez_compressed(HERE / 'config2_talker64.npz', **expected_config2())
+    np.savez_compressed(HERE / 'prefill16.npz', **expected_prefill())
     (HERE / 'scheduler_trace.json').write_text(json.dumps(expected_scheduler(), separators=(',', ':')))
     for p in sorted(HERE.glob('*.*')):
         print(p.name, p.stat().st_size)

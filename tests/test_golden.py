@@ -52,6 +52,17 @@ def test_config2_golden_reproduced():
     np.testing.assert_allclose(g["out"], now["out"], atol=1e-6, rtol=0)
 
 
+def test_prefill_golden_reproduced():
+    g = load("prefill16.npz")
+    now = mg.expected_prefill()
+    assert int(g["lengths"].sum()) == 4790
+    for key in ("lengths", "last_tokens"):
+        assert np.array_equal(g[key], now[key]), key
+    for key in ("keys_sha256", "values_sha256"):
+        assert str(g[key]) == str(now[key]), key
+    np.testing.assert_allclose(g["out_last"], now["out_last"], atol=1e-6, rtol=0)
+
+
 @pytest.mark.parametrize("run", range(len(mg.SCHEDULER_SETTINGS)))
 def test_scheduler_golden_reproduced_by_oracle_and_package(pkg, run):
     from qwen3_tts_engine_amd.scheduler import SlotScheduler

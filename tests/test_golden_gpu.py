@@ -67,3 +67,22 @@ def test_config2_golden_fused_step(pkg, device, max_chunks):
     assert hashlib.sha256(bits(dv).tobytes()).hexdigest() == str(g["values_sha256"])
     selected = torch.from_numpy(g["selected"]).to(device)
     assert_attention_close(f64(out.index_select(0, selected)), g["out"].astype(np.float64))
+
+
+def test_prefill_golden(pkg, device):
+    """The 16-prompt prefill through prefill_step (keys/values prologue, attention rotating the
+    raw queries): the arena bit-exact, each prompt's last-token output within the bf16 bar."""
+    g = load("prefill16.npz")
+    lengths, cu, positions, q, k, v = mg.prefill_inputs()
+    assert np.array_equal(lengths, g["lengths"])
+    cos_b, sin_b = mg.prefill_tables(positions)
+    cos, sin = from_bits(cos_b, device), from_bits(sin_b, device)
+    ak = torch.zeros(mg.PREFILL_SLOTS, mg.HKV, mg.PREFILL_CAPACITY, mg.D, device=device, dtype=torch.bfloat16)
+    av = torch.zeros_like(ak)
+    dcu = torch.from_numpy(cu).to(device)
+    out = pkg.prefill_step(q.to(device), k.to(device), v.to(device), cos, sin, dcu, int(lengths.max()), ak, av)
+    torch.cuda.synchronize()
+    assert hashlib.sha256(bits(ak).tobytes()).hexdigest() == str(g["keys_sha256"])
+    assert hashlib.sha256(bits(av).tobytes()).hexdigest() == str(g["values_sha256"])
+    last = torch.from_numpy(g["last_tokens"]).to(device)
+    assert_attention_close(f64(out.index_select(0, last)), g["out_last"].astype(np.float64))
