@@ -40,8 +40,9 @@ def rope_bf16(x_bits, cos_bits, sin_bits):
     half = x.shape[-1] // 2
     x1, x2 = x[..., :half], x[..., half:]
     c1, c2, s1, s2 = c[..., :half], c[..., half:], s[..., :half], s[..., half:]
-    y1 = bf16.to_bits(bf16.round_bf16(x1 * c1) + bf16.round_bf16(-(x2 * s1)))
-    y2 = bf16.to_bits(bf16.round_bf16(x2 * c2) + bf16.round_bf16(x1 * s2))
+    with np.errstate(over='ignore', invalid='ignore'):  # inf/NaN inputs propagate as IEEE says
+        y1 = bf16.to_bits(bf16.round_bf16(x1 * c1) + bf16.round_bf16(-(x2 * s1)))
+        y2 = bf16.to_bits(bf16.round_bf16(x2 * c2) + bf16.round_bf16(x1 * s2))
     return np.concatenate([y1, y2], axis=-1)
 
 
