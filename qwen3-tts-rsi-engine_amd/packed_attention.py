@@ -44,6 +44,7 @@ from .slots import PredictorCache, SlotCache
 _ATTENTION_CLASSES = ('Qwen3TTSTalkerAttention', 'Qwen3TTSAttention')
 
 _CAUSAL_PAIR: dict = {}
+_CAUSAL_PAIR_LIMIT = 64
 
 
 def _is_causal_pair(mask, batch):
@@ -66,7 +67,10 @@ def _is_causal_pair(mask, batch):
         low = torch.finfo(mask.dtype).min
         causal = bool((values[..., 0, 0] == 0).all() and (values[..., 1, 0] == 0).all()
                       and (values[..., 1, 1] == 0).all() and (values[..., 0, 1] <= low).all())
-        # the entry keeps the mask alive, so its address cannot be reused by another tensor
+        # the entry keeps the mask alive, so its address cannot be reused by another tensor;
+        # the oldest entries go once a caller has shown many distinct masks
+        if len(_CAUSAL_PAIR) >= _CAUSAL_PAIR_LIMIT:
+            del _CAUSAL_PAIR[next(iter(_CAUSAL_PAIR))]
         seen = _CAUSAL_PAIR[key] = (causal, mask)
     return seen[0]
 
