@@ -150,6 +150,105 @@ def predictor_detail(pkg, device, reps=20):
             "us_per_layer_step": chain_us / (steps * layers)}
 
 
+def _replay_us(fn, calls=1, reps=100):
+    """Mean time per call of a graph holding ``calls`` calls of ``fn``, over ``reps`` replays
+    after warm-up, launch included.  With one call this is the method of the reference's
+    operator probes (tools/probe_attention_context.py:48-65, tools/probe_rotary_exact.py:69-74);
+    more calls per graph spread the graph launch over them."""
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(calls):
+            fn()
+    for _ in range(10):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    return round(start.elapsed_time(stop) * 1e3 / (reps * calls), 2)
+
+
+def reference_probe_detail(pkg, device):
+    """The reference's own operator probes at their B=64 shapes (its Ascend 910B1 figures in
+    ``reference_910b1_us``), same inputs, timed as one call per graph (the reference's method)
+    and as 20 calls per graph:
+
+    * decode GQA, 16/8 heads, D 128, a 512-row arena, positions (7 b) mod L
+      (tools/probe_attention_context.py:20-36): with the boolean mask over all 512 keys
+      (``full_arena``), with the mask and L valid keys (``valid_length``), and through
+      positions alone (``positions``, the form the slot cache uses); all three give the
+      same output;
+    * the paired K/V write from strided projection views, capacity 512
+      (tools/probe_paired_kv.py:24-38);
+    * exact bf16 RoPE of q and k, BSND, cos/sin from random phases
+      (tools/probe_rotary_exact.py:23-37);
+    * predictor-shape attention, D 64 in a 16-row cache with L valid keys, the 2x2 causal
+      step at L = 2 (tools/probe_predictor_padded_kv.py:20-35).
+
+    ``graph_replay_floor_us`` is one replay of a graph holding a single one-element add."""
+    gen = torch.Generator(device=device).manual_seed(42)
+    probes = {}
+    diffs = {}
+    for batch, lengths in ((64, (64, 128, 256, 512)), (32, (512,)), (8, (512,)), (1, (512,))):
+        q = torch.randn(batch, 1, HQ, D, generator=gen, device=device, dtype=torch.bfloat16)
+        keys = torch.randn(batch, HKV, 512, D, generator=gen, device=device, dtype=torch.bfloat16)
+        values = torch.randn_like(keys)
+        for length in lengths:
+            positions = (torch.arange(batch, device=device) * 7) % length
+            keep = (torch.arange(512, device=device)[None, :] <= positions[:, None])[:, None, None, :]
+            full = torch.full((batch,), 511, device=device, dtype=torch.int64)
+            valid = torch.full((batch,), length - 1, device=device, dtype=torch.int64)
+            calls = {"full_arena": (pkg.decode_attention, (q, keys, values, full), {"mask": keep}),
+                     "valid_length": (pkg.decode_attention, (q, keys, values, valid), {"mask": keep}),
+                     "positions": (pkg.decode_attention, (q, keys, values, positions), {})}
+            outs = [fn(*a, **kw).float() for fn, a, kw in calls.values()]
+            diffs[f"decode_gqa_b{batch}_L{length}"] = max(float((o - outs[0]).abs().max()) for o in outs[1:])
+            for name, call in calls.items():
+                probes[f"decode_gqa_b{batch}_L{length}_{name}"] = call
+    batch, capacity = 64, 512
+    packed = torch.randn(batch, 1, (HQ + 2 * HKV) * D, generator=gen, device=device, dtype=torch.bfloat16)
+    k = packed[..., HQ * D:(HQ + HKV) * D].view(batch, 1, HKV, D).transpose(1, 2)
+    v = packed[..., (HQ + HKV) * D:].view(batch, 1, HKV, D).transpose(1, 2)
+    cache = [torch.randn(batch, HKV, capacity, D, generator=gen, device=device, dtype=torch.bfloat16)
+             for _ in range(2)]
+    positions = torch.arange(batch, device=device) % capacity
+    probes["paired_kv_write_b64_cap512"] = (pkg.write, (k, v, *cache, positions), {"row_tiled": True})
+    for length in (1, 64):
+        query = torch.randn(batch, length, HQ, D, generator=gen, device=device, dtype=torch.bfloat16)
+        key = torch.randn(batch, length, HKV, D, generator=gen, device=device, dtype=torch.bfloat16)
+        phase = torch.randn(batch, length, D // 2, generator=gen, device=device).repeat(1, 1, 2)
+        cos, sin = phase.cos().bfloat16(), phase.sin().bfloat16()
+        probes[f"rope_qk_b64_s{length}"] = (
+            lambda qq, kk, c, s: (pkg.rotary(qq, c, s), pkg.rotary(kk, c, s)), (query, key, cos, sin), {})
+    for length in (2, 3, 8, 16):
+        qlen = 2 if length == 2 else 1
+        q = torch.randn(batch, qlen, HQ, 64, generator=gen, device=device, dtype=torch.bfloat16)
+        keys = torch.randn(batch, HKV, 16, 64, generator=gen, device=device, dtype=torch.bfloat16)
+        values = torch.randn_like(keys)
+        valid = torch.full((batch,), length - 1, device=device, dtype=torch.int64)
+        probes[f"predictor_attention_b64_L{length}"] = (pkg.decode_attention, (q, keys, values, valid), {})
+    out = {}
+    for calls in (1, 20):
+        out[f"{calls}_call_per_graph_us" if calls == 1 else f"{calls}_calls_per_graph_us"] = {
+            name: _replay_us(lambda: fn(*a, **kw), calls=calls) for name, (fn, a, kw) in probes.items()}
+    one = torch.zeros(1, device=device)
+    out["graph_replay_floor_us"] = _replay_us(lambda: one.add_(1))
+    out["decode_gqa_max_abs_diff_between_forms"] = diffs
+    out["reference_910b1_us"] = {
+        "decode_gqa_b64_L512": {"full_arena": 99.13, "valid_length": 99.16},
+        "decode_gqa_b64_L64/128/256_valid_length": [86.70, 86.50, 90.31],
+        "decode_gqa_b32/b8/b1_L512_full_arena": [64.98, 43.73, 22.91],
+        "paired_kv_write_b64_cap512": 11.54, "rope_qk_b64_s1": 23.61, "rope_qk_b64_s64": 90.57,
+        "predictor_attention_b64_L2/3/8/16": [77.19, 77.28, 76.84, 79.23]}
+    return out
+
+
 def read_traffic():
     """HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (committed summary)."""
     if not TRAFFIC_SUMMARY.exists():
@@ -373,7 +472,8 @@ def main():
                  "arena_move": arena_move_detail(pkg, arena, contexts),
                  "talker_attention_step": slot_graph_detail(pkg, device, contexts),
                  "talker_attention_step_fused_qk_norm": slot_graph_detail(pkg, device, contexts,
-                                                                          fused_qk_norm=True)}
+                                                                          fused_qk_norm=True),
+                 "reference_probe_shapes": reference_probe_detail(pkg, device)}
     traffic = read_traffic()
     result = {
         "metric": "decode-attn tokens/s + achieved HBM GB/s, 64-req ragged talker step, 1 GPU",

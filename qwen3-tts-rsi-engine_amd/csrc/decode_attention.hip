@@ -247,11 +247,15 @@ struct DecodeShape {
 // Waves per SIMD the register allocation aims for: the kernel is latency-bound, so the
 // bf16 variants with at most two query rows per KV head are held to 80 VGPRs (6 waves),
 // which they meet without spilling; wider variants keep the compiler's choice.
-constexpr int decode_waves_per_eu(int es, int rows) { return es == 2 && rows <= 2 ? 6 : 1; }
+// bf16 launches of one or two query rows per KV head fit 80 VGPRs (6 waves per SIMD); the
+// mask's per-key terms need a few more, which 5 waves per SIMD leave room for without spills
+constexpr int decode_waves_per_eu(int es, int rows, bool mask) {
+    return es == 2 && rows <= 2 ? (mask ? 5 : 6) : 1;
+}
 
 template <typename T, int D, int G, int SQ, bool FUSED, bool MASK, bool STREAM>
 __global__ void __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(decode_waves_per_eu(sizeof(T), G * SQ))))
+__attribute__((amdgpu_waves_per_eu(decode_waves_per_eu(sizeof(T), G * SQ, MASK))))
 decode_attention_kernel(DecodeParams p) {
     constexpr int R = G * SQ;
     using S = DecodeShape<T, D>;
@@ -361,7 +365,7 @@ decode_attention_kernel(DecodeParams p) {
 
     // one online-softmax step over P key vectors per lane (invalid ones carry -inf scores)
     auto step = [&](const U4 (&kr)[P], const U4 (&vr)[P], const int (&kidx)[P], const bool (&valid)[P],
-                    bool rescale) {
+                    const float (&mk)[P][SQ], bool rescale) {
         float s[P][R];
 #pragma unroll
         for (int pp = 0; pp < P; ++pp)
@@ -372,13 +376,7 @@ decode_attention_kernel(DecodeParams p) {
                 // several queries of a request without a mask: causal among the last keys
                 if constexpr (SQ > 1 && !MASK) ok = ok && kidx[pp] <= L - SQ + qi;
                 float x = group_sum<LPK>(lane_dot<T>(qr[r], kr[pp])) * p.scale_log2;
-                if constexpr (MASK) {
-                    if (ok) {
-                        const char *mp = mask_row + (qi * p.m_ss + (int64_t)kidx[pp] * p.m_st) *
-                                                        mask_elem_size(p.mask_dtype);
-                        x += load_mask(mp, p.mask_dtype) * kLog2e;
-                    }
-                }
+                if constexpr (MASK) x += mk[pp][qi];
                 s[pp][r] = ok ? x : -INFINITY;
             }
 #pragma unroll
@@ -437,19 +435,38 @@ decode_attention_kernel(DecodeParams p) {
             valid[pp] = kidx[pp] < jend;
         }
     };
+    // mask terms of the block's keys (log2 units), requested right after the block's key and
+    // value rows so that the scores wait for one round trip, not two
+    auto block_mask = [&](const int (&kidx)[P], const bool (&valid)[P], float (&mk)[P][SQ]) {
+#pragma unroll
+        for (int pp = 0; pp < P; ++pp)
+#pragma unroll
+            for (int qi = 0; qi < SQ; ++qi) {
+                mk[pp][qi] = 0.f;
+                if constexpr (MASK) {
+                    if (valid[pp])
+                        mk[pp][qi] = load_mask(mask_row + (qi * p.m_ss + (int64_t)kidx[pp] * p.m_st) *
+                                                              mask_elem_size(p.mask_dtype),
+                                               p.mask_dtype) * kLog2e;
+                }
+            }
+    };
     for (int jb = j0; jb < jend; jb += kChunkRows) {
         U4 kr[P], vr[P];
         int kidx[P];
         bool valid[P];
+        float mk[P][SQ];
         load_block(jb, kr, vr);
         block_keys(jb, kidx, valid);
-        step(kr, vr, kidx, valid, jb != j0);
+        block_mask(kidx, valid, mk);
+        step(kr, vr, kidx, valid, mk, jb != j0);
     }
     if constexpr (FUSED) {
         if (with_new && wave == 0) {  // the new keys: token t's in lane group t of wave 0
             U4 kr[P], vr[P];
             int kidx[P];
             bool valid[P];
+            float mk[P][SQ] = {};
             const U4 zero = {0u, 0u, 0u, 0u};
             const bool mine = grp < SQ && L - SQ + grp >= 0;
 #pragma unroll
@@ -459,7 +476,7 @@ decode_attention_kernel(DecodeParams p) {
                 kidx[pp] = L - SQ + grp;
                 valid[pp] = pp == 0 && mine;
             }
-            step(kr, vr, kidx, valid, j0 < jend);
+            step(kr, vr, kidx, valid, mk, j0 < jend);
         }
     }
 
@@ -604,8 +621,8 @@ extern "C" int64_t q3t_decode_workspace_bytes(int64_t batch, int64_t query_len, 
 template <typename T, int D, int G, int SQ, bool F, bool M>
 static void launch_decode(const DecodeParams &p, hipStream_t s) {
     const dim3 grid((uint32_t)p.B * p.Hkv * p.nchunks);
-    // streamed instances only for the talker-shaped single-query launches without a mask
-    if constexpr (sizeof(T) == 2 && D == 128 && SQ == 1 && !M) {
+    // streamed instances only for the talker-shaped single-query launches
+    if constexpr (sizeof(T) == 2 && D == 128 && SQ == 1) {
         if (p.stream) {
             hipLaunchKernelGGL((decode_attention_kernel<T, D, G, SQ, F, M, true>), grid, dim3(kThreads), 0, s, p);
             return;

@@ -232,6 +232,27 @@ def test_mask_matches_sdpa_semantics(pkg, device, kind):
     assert_attention_close(f64(out), expected)
 
 
+@pytest.mark.parametrize("kind", ["bool", "additive_bf16"])
+def test_masked_full_arena_probe_shape(pkg, device, kind):
+    """The reference's attention-context probe (tools/probe_attention_context.py:20-36): 64
+    requests over a 512-row arena, positions (7 b) mod 512, the mask over all 512 keys; the
+    launch reads more than 16 MB, so it takes the non-temporal loads."""
+    batch, capacity = 64, 512
+    k, v = _arena(batch, capacity, torch.bfloat16, device, 31)
+    gen = torch.Generator().manual_seed(32)
+    q = torch.randn(batch, 1, HQ, D, generator=gen).bfloat16().to(device)
+    positions = (torch.arange(batch) * 7) % capacity
+    allowed = torch.arange(capacity)[None, :] <= positions[:, None]
+    if kind == "bool":
+        mask = allowed
+    else:
+        mask = torch.where(allowed, 0.0, torch.finfo(torch.bfloat16).min).bfloat16()
+    full = torch.full((batch,), capacity - 1, dtype=torch.int64, device=device)
+    out = pkg.decode_attention(q, k, v, full, mask=mask[:, None, None].to(device))
+    expected = oatt.decode_attention(f64(q), f64(k), f64(v), positions.numpy(), D ** -0.5)
+    assert_attention_close(f64(out), expected)
+
+
 def test_trimmed_context_equals_masked_arena(pkg, device):
     """tests/test_slot_context.py:32-36: attention over the trimmed context equals
     attention over the full arena under the j <= pos mask."""
