@@ -33,47 +33,51 @@ Q3T_DEVICE int request_of(const int32_t *cu, int B, int64_t t) {
     return lo;
 }
 
-// One work item: 8 dims of each half of one (token, head) row.  Heads [0, Hq) are query
-// heads (rotated into q_out; absent when q_out is null, the attention kernel then rotates
-// the queries itself); the Hkv heads after them rotate the key and copy the value into the
-// arena at the token's position within its request.
+// One wave per token; a lane's work item is 8 dims of each half of one of the token's head
+// rows.  Heads [0, Hq) are query heads (rotated into q_out; absent when q_out is null, the
+// attention kernel then rotates the queries itself); the Hkv heads after them rotate the key
+// and copy the value into the arena at the token's position within its request.  The token's
+// request, position and slot are the same for the whole wave (scalar loads): 12.5 -> 12.0 us
+// per layer on the 16-prompt workload against one item per thread with per-lane lookups.
 __global__ void __launch_bounds__(256) prefill_rope_write_kernel(PrefillRopeWriteParams p) {
     const int vecs = p.D / 16;
     const int qh = p.qo ? p.Hq : 0;  // without q_out only the key/value rows are handled
-    const int heads = qh + p.Hkv;
-    const int64_t total = p.T * heads * vecs;
+    const int items = (qh + p.Hkv) * vecs;
     const int half = p.D / 2;
-    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        const int c = (int)(i % vecs);
-        const int64_t th = i / vecs;
-        const int hd = (int)(th % heads);
-        const int64_t t = th / heads;
-        const char *crow = p.cs + t * p.cs_st * 2, *srow = p.sn + t * p.cs_st * 2;
-        U4 c1 = load16(crow + c * 16), c2 = load16(crow + (half + c * 8) * 2);
-        U4 s1 = load16(srow + c * 16), s2 = load16(srow + (half + c * 8) * 2);
-        if (hd < qh) {
-            const char *row = p.q + (t * p.q_st + hd * p.q_sh) * 2;
-            U4 x1 = load16(row + c * 16), x2 = load16(row + (half + c * 8) * 2), y1, y2;
-            rope8(&x1.x, &x2.x, &c1.x, &c2.x, &s1.x, &s2.x, &y1.x, &y2.x);
-            char *orow = p.qo + (t * p.qo_st + hd * p.qo_sh) * 2;
-            store16(orow + c * 16, y1);
-            store16(orow + (half + c * 8) * 2, y2);
-        } else {
-            const int h = hd - qh;
-            const int b = request_of(p.cu, p.B, t);
-            const int64_t pos = t - p.cu[b];
-            if (pos < 0 || pos >= p.capacity) continue;
-            const int64_t slot = p.slots ? p.slots[b] : b;
-            const char *krow = p.k + (t * p.k_st + h * p.k_sh) * 2;
-            const char *vrow = p.v + (t * p.v_st + h * p.v_sh) * 2;
-            U4 x1 = load16(krow + c * 16), x2 = load16(krow + (half + c * 8) * 2), y1, y2;
-            rope8(&x1.x, &x2.x, &c1.x, &c2.x, &s1.x, &s2.x, &y1.x, &y2.x);
-            const int64_t a = (slot * p.a_sb + h * p.a_sh + pos * p.a_st) * 2;
-            store16(p.ak + a + c * 16, y1);
-            store16(p.ak + a + (half + c * 8) * 2, y2);
-            store16(p.av + a + c * 16, load16(vrow + c * 16));
-            store16(p.av + a + (half + c * 8) * 2, load16(vrow + (half + c * 8) * 2));
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    for (int t = blockIdx.x * 4 + wave; t < (int)p.T; t += gridDim.x * 4) {
+        // the token is the same for the whole wave: its request, position and slot come from
+        // scalar loads
+        const int b = request_of(p.cu, p.B, t);
+        const int pos = t - p.cu[b];
+        const bool write_kv = pos >= 0 && pos < p.capacity;
+        const int64_t slot = p.slots ? p.slots[b] : b;
+        const char *crow = p.cs + (int64_t)t * p.cs_st * 2, *srow = p.sn + (int64_t)t * p.cs_st * 2;
+        for (int it = lane; it < items; it += 64) {
+            const int c = it % vecs, hd = it / vecs;
+            U4 c1 = load16(crow + c * 16), c2 = load16(crow + (half + c * 8) * 2);
+            U4 s1 = load16(srow + c * 16), s2 = load16(srow + (half + c * 8) * 2);
+            if (hd < qh) {
+                const char *row = p.q + ((int64_t)t * p.q_st + hd * p.q_sh) * 2;
+                U4 x1 = load16(row + c * 16), x2 = load16(row + (half + c * 8) * 2), y1, y2;
+                rope8(&x1.x, &x2.x, &c1.x, &c2.x, &s1.x, &s2.x, &y1.x, &y2.x);
+                char *orow = p.qo + ((int64_t)t * p.qo_st + hd * p.qo_sh) * 2;
+                store16(orow + c * 16, y1);
+                store16(orow + (half + c * 8) * 2, y2);
+            } else if (write_kv) {
+                const int h = hd - qh;
+                const char *krow = p.k + ((int64_t)t * p.k_st + h * p.k_sh) * 2;
+                const char *vrow = p.v + ((int64_t)t * p.v_st + h * p.v_sh) * 2;
+                U4 x1 = load16(krow + c * 16), x2 = load16(krow + (half + c * 8) * 2), y1, y2;
+                const U4 w1 = load16(vrow + c * 16), w2 = load16(vrow + (half + c * 8) * 2);
+                rope8(&x1.x, &x2.x, &c1.x, &c2.x, &s1.x, &s2.x, &y1.x, &y2.x);
+                const int64_t a = (slot * p.a_sb + h * p.a_sh + pos * p.a_st) * 2;
+                store16(p.ak + a + c * 16, y1);
+                store16(p.ak + a + (half + c * 8) * 2, y2);
+                store16(p.av + a + c * 16, w1);
+                store16(p.av + a + (half + c * 8) * 2, w2);
+            }
         }
     }
 }
@@ -458,6 +462,7 @@ extern "C" int q3t_prefill_rope_write(const q3t_prefill_rope_write_args *a, void
         a->capacity < 1 || a->batch > (1 << 20))
         return Q3T_EINVAL;
     if (a->head_dim != 64 && a->head_dim != 128) return Q3T_EUNSUPPORTED;
+    if (a->total_tokens > (1 << 30)) return Q3T_EUNSUPPORTED;  // 32-bit token indices
     if (a->total_tokens == 0) return Q3T_OK;
     // q_out == NULL: keys and values only (the attention kernel rotates the queries itself)
     const bool with_q = a->q_out != nullptr;
@@ -484,8 +489,7 @@ extern "C" int q3t_prefill_rope_write(const q3t_prefill_rope_write_args *a, void
     p.ak = (char *)a->arena_keys; p.av = (char *)a->arena_values;
     p.a_sb = a->a_stride_b; p.a_sh = a->a_stride_h; p.a_st = a->a_stride_t;
     p.slots = a->kv_slots;
-    const int64_t total = p.T * ((with_q ? p.Hq : 0) + p.Hkv) * (p.D / 16);
-    int64_t blocks = (total + 255) / 256;
+    int64_t blocks = (p.T + 3) / 4;  // one token per wave
     if (blocks > 16384) blocks = 16384;
     hipLaunchKernelGGL(prefill_rope_write_kernel, dim3((unsigned)blocks), dim3(256), 0,
                        (hipStream_t)stream, p);
