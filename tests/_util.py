@@ -19,7 +19,7 @@ def f64(t: torch.Tensor) -> np.ndarray:
 
 
 def assert_attention_close(actual, expected, max_abs=2e-2, mean_abs=2e-3):
-    """The north-star tolerance: max-abs <= 2e-2 and mean-abs <= 2e-3 (bf16 I/O, fp32 acc)."""
+    """The attention tolerance: max-abs <= 2e-2 and mean-abs <= 2e-3 (bf16 I/O, fp32 acc)."""
     actual = np.asarray(actual, dtype=np.float64)
     err = np.abs(actual - expected)
     assert np.isfinite(actual).all(), "non-finite attention output"
