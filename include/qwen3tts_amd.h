@@ -39,10 +39,13 @@ extern "C" {
 #define Q3T_F32 2
 #define Q3T_BOOL 3  /* masks only: nonzero = attend, as a torch bool SDPA mask */
 
-/* Human-readable text for a status returned by any entry point. */
+/* Human-readable text for a status returned by any entry point.  The reference's wrappers
+   raise ValueError with such a text before launching (kv_triton_ascend.py:40-53); the
+   Python bindings here do the same with this string. */
 const char *q3t_status_string(int status);
 
-/* ABI revision of this header; bumps on any incompatible change. */
+/* ABI revision of this header; bumps on any incompatible change.  No counterpart in the
+   reference (its operators are Python functions); the bindings refuse another revision. */
 int q3t_abi_version(void);
 
 /* ---- KV arena writes and copies ------------------------------------------------------ */
@@ -77,7 +80,8 @@ int q3t_copy_strided(void *dst, const void *src, int64_t elem_size, int ndim,
                      const int64_t *sizes, const int64_t *dst_strides,
                      const int64_t *src_strides, void *stream);
 
-/* Plain contiguous byte copy (also the calibration kernel for HBM counters). */
+/* Plain contiguous byte copy: the calibration kernel for the HBM byte counters (a copy of
+   known size).  No counterpart in the reference; slot moves go through q3t_copy_strided. */
 int q3t_copy_bytes(void *dst, const void *src, int64_t nbytes, void *stream);
 
 /* ---- rotary position embedding ------------------------------------------------------ */
@@ -178,7 +182,9 @@ typedef struct q3t_decode_args {
     int64_t nk_stride_s, nv_stride_s, cs_stride_s;
 } q3t_decode_args;
 
-/* Bytes of workspace needed by q3t_decode_attention for these sizes. */
+/* Bytes of workspace needed by q3t_decode_attention for these sizes.  No counterpart in
+   the reference (its attention operator allocates internally); callers size the buffer
+   once, outside graph capture. */
 int64_t q3t_decode_workspace_bytes(int64_t batch, int64_t query_len, int64_t q_heads,
                                    int64_t kv_heads, int64_t head_dim, int64_t ctx,
                                    int64_t max_chunks);
