@@ -368,6 +368,46 @@ def test_attention_dropin_signature_and_errors(pkg, device):
         pkg.attention(module, q, k, v, None)
 
 
+@pytest.mark.parametrize("batch,length", [(64, 64), (64, 256), (8, 512), (1, 128)])
+def test_valid_length_dropin_with_poisoned_tail_and_replays(pkg, device, batch, length):
+    """tools/probe_attention_context.py:20-60: 16/8 heads over a 512-row arena, positions
+    (7 b) mod L, the mask over all 512 keys, with and without actual_seq_lengths_kv = [L]*B.
+    Rows from L on are poisoned before every replay of the captured valid-length call; each
+    replay must equal the eager full-mask call, and both the oracle."""
+    class Module:
+        training = False
+        sliding_window = None
+
+    gen = torch.Generator(device=device).manual_seed(60 + length)
+    q = torch.randn(batch, HQ, 1, D, generator=gen, device=device, dtype=torch.bfloat16)
+    k = torch.randn(batch, HKV, 512, D, generator=gen, device=device, dtype=torch.bfloat16)
+    v = torch.randn_like(k)
+    positions = (torch.arange(batch) * 7) % length
+    allowed = torch.arange(512)[None, :] <= positions[:, None]
+    mask = allowed[:, None, None, :].to(device)
+    lengths = [length] * batch
+
+    def valid():
+        return pkg.attention(Module(), q, k, v, mask, scaling=D ** -0.5, actual_seq_lengths_kv=lengths)[0]
+
+    expected = oatt.decode_attention(f64(q.transpose(1, 2)), f64(k), f64(v), positions.numpy(), D ** -0.5)
+    assert_attention_close(f64(valid()), expected)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = valid()
+    for replay in range(3):
+        q.copy_(torch.randn(q.shape, generator=gen, device=device, dtype=torch.bfloat16))
+        k[:, :, length:].fill_(100 * (replay + 1))
+        v[:, :, length:].fill_(-100 * (replay + 1))
+        graph.replay()
+        full = pkg.attention(Module(), q, k, v, mask, scaling=D ** -0.5)[0]
+        torch.cuda.synchronize()
+        assert torch.equal(captured, full)
+    expected = oatt.decode_attention(f64(q.transpose(1, 2)), f64(k), f64(v), positions.numpy(), D ** -0.5)
+    assert_attention_close(f64(captured), expected)
+
+
 @pytest.mark.parametrize("kv_heads,max_chunks", [(8, 0), (4, 5), (8, 2)])
 def test_split_merge_is_deterministic_across_launches(pkg, device, kv_heads, max_chunks):
     """Chunk states cross workgroups (and, with 4 KV heads, XCDs) through the workspace;
