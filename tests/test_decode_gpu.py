@@ -408,6 +408,40 @@ def test_valid_length_dropin_with_poisoned_tail_and_replays(pkg, device, batch, 
     assert_attention_close(f64(captured), expected)
 
 
+@pytest.mark.parametrize("length", [2, 3, 8, 16])
+def test_predictor_padded_cache_equals_sliced(pkg, device, length):
+    """tools/probe_predictor_padded_kv.py:20-60: head_dim 64 in a 16-row cache, two queries
+    under the first step's mask at length 2 (query 0 sees key 0 only), one query otherwise;
+    the padded call (actual_seq_lengths_kv, poisoned rows past the length) equals the call
+    on the sliced cache, and both the oracle."""
+    class Module:
+        training = False
+        sliding_window = None
+
+    batch, head_dim = 64, 64
+    qlen = 2 if length == 2 else 1
+    gen = torch.Generator(device=device).manual_seed(70 + length)
+    q = torch.randn(batch, HQ, qlen, head_dim, generator=gen, device=device, dtype=torch.bfloat16)
+    k = torch.randn(batch, HKV, 16, head_dim, generator=gen, device=device, dtype=torch.bfloat16)
+    v = torch.randn_like(k)
+    k[:, :, length:].fill_(100)
+    v[:, :, length:].fill_(-100)
+    keep = torch.ones(1, 1, qlen, 16, dtype=torch.bool)
+    if qlen == 2:
+        keep[..., 0, 1:] = False
+    keep = keep.to(device)
+    scale = head_dim ** -0.5
+    padded = pkg.attention(Module(), q, k, v, keep, scaling=scale, actual_seq_lengths_kv=[length] * batch)[0]
+    sliced = pkg.attention(Module(), q, k[:, :, :length].contiguous(), v[:, :, :length].contiguous(),
+                           keep[..., :length].contiguous(), scaling=scale)[0]
+    torch.cuda.synchronize()
+    assert torch.equal(padded, sliced)
+    allowed = keep[0, 0, :, :length].cpu().numpy()[None].repeat(batch, 0)
+    expected = oatt.decode_attention(f64(q.transpose(1, 2)), f64(k[:, :, :length]), f64(v[:, :, :length]),
+                                     np.full(batch, length - 1), scale, mask=allowed)
+    assert_attention_close(f64(padded), expected)
+
+
 @pytest.mark.parametrize("kv_heads,max_chunks", [(8, 0), (4, 5), (8, 2)])
 def test_split_merge_is_deterministic_across_launches(pkg, device, kv_heads, max_chunks):
     """Chunk states cross workgroups (and, with 4 KV heads, XCDs) through the workspace;
