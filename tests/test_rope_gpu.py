@@ -64,3 +64,37 @@ def test_rope_tables_talker_positions(pkg, device):
     f32cos, _ = pkg.rope_tables(positions.to(device), 128, dtype=torch.float32)
     ref32, _ = orope.tables(positions.numpy(), inv.numpy(), dtype="f32")
     assert np.abs(f32cos.cpu().numpy() - ref32).max() <= 2.5e-7
+
+
+@pytest.mark.parametrize("length", [1, 64])
+def test_rotary_graph_replays_track_inputs(pkg, device, length):
+    """tools/probe_rotary_exact.py:41-61: q and k rotated by one captured graph; the inputs
+    and the cos/sin rows are overwritten in place before each of three replays, and every
+    replay must be bit-exact for the new inputs."""
+    batch = 17
+    gen = torch.Generator(device=device).manual_seed(43)
+    q = torch.empty(batch, length, 16, 128, device=device, dtype=torch.bfloat16)
+    k = torch.empty(batch, length, 8, 128, device=device, dtype=torch.bfloat16)
+    cos = torch.empty(batch, length, 128, device=device, dtype=torch.bfloat16)
+    sin = torch.empty_like(cos)
+
+    def refill():
+        for t in (q, k):
+            t.copy_(torch.randn(t.shape, generator=gen, device=device))
+        phase = torch.randn(batch, length, 64, generator=gen, device=device).repeat(1, 1, 2)
+        cos.copy_(phase.cos())
+        sin.copy_(phase.sin())
+
+    refill()
+    pkg.rotary(q, cos, sin), pkg.rotary(k, cos, sin)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outputs = (pkg.rotary(q, cos, sin), pkg.rotary(k, cos, sin))
+    for _ in range(3):
+        refill()
+        graph.replay()
+        torch.cuda.synchronize()
+        c, s = bits(cos)[:, :, None, :], bits(sin)[:, :, None, :]
+        for x, y in zip((q, k), outputs):
+            assert np.array_equal(bits(y), orope.rope_bf16(bits(x), c, s))
