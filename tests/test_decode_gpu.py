@@ -408,6 +408,43 @@ def test_valid_length_dropin_with_poisoned_tail_and_replays(pkg, device, batch, 
     assert_attention_close(f64(captured), expected)
 
 
+@pytest.mark.parametrize("batch,qlen,kvlen", [(1, 2, 2), (1, 1, 16), (4, 1, 512), (32, 1, 512)])
+def test_mask_rewritten_between_replays_is_seen(pkg, device, batch, qlen, kvlen):
+    """tools/probe_gqa_operator.py:31-58: one captured attention call with a boolean mask;
+    before each replay the queries are redrawn and the mask is rewritten in place (a
+    different key hidden from query 0), so frozen arguments would show."""
+    class Module:
+        training = False
+        sliding_window = None
+
+    gen = torch.Generator(device=device).manual_seed(80 + kvlen)
+    q = torch.randn(batch, HQ, qlen, D, generator=gen, device=device, dtype=torch.bfloat16)
+    k = torch.randn(batch, HKV, kvlen, D, generator=gen, device=device, dtype=torch.bfloat16)
+    v = torch.randn_like(k)
+    keep = torch.ones(batch, 1, qlen, kvlen, device=device, dtype=torch.bool)
+    keep[..., 0, -1] = False
+
+    def call():
+        return pkg.attention(Module(), q, k, v, keep, scaling=D ** -0.5)[0]
+
+    call()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = call()
+    for replay in range(3):
+        q.copy_(torch.randn(q.shape, generator=gen, device=device, dtype=torch.bfloat16))
+        keep.fill_(True)
+        keep[..., 0, -(replay % kvlen + 1)] = False
+        graph.replay()
+        eager = call()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager)
+        expected = oatt.decode_attention(f64(q.transpose(1, 2)), f64(k), f64(v), np.full(batch, kvlen - 1),
+                                         D ** -0.5, mask=keep[:, 0].cpu().numpy())
+        assert_attention_close(f64(captured), expected)
+
+
 @pytest.mark.parametrize("length", [2, 3, 8, 16])
 def test_predictor_padded_cache_equals_sliced(pkg, device, length):
     """tools/probe_predictor_padded_kv.py:20-60: head_dim 64 in a 16-row cache, two queries
