@@ -199,3 +199,37 @@ def test_prefill_rejects_bad_arguments(pkg, device):
         pkg.prefill_rope_write(q, k, k, cos[:5], cos[:5], cu, ak, ak)
     with pytest.raises(ValueError):
         pkg.prefill_rope_write(q, k, k, cos, cos, cu, ak[:1], ak[:1])
+
+
+def test_prefill_request_order_does_not_change_results(pkg, device):
+    """tools/probe_prefill_graph.py:29-55 replays the same prompts in orders [0, 1, 2, 3] and
+    [3, 0, 1, 2]: each prompt's arena rows and attention rows must not depend on where it
+    sits in the packed batch (bit for bit), with every prompt keeping its slot."""
+    lengths = [37, 200, 64, 129]
+    q_heads, kv_heads, head_dim, capacity = 16, 8, 128, 256
+    q, k, v, cu, positions = _packed(lengths, q_heads, kv_heads, head_dim, 11)
+    cos_b, sin_b = _tables(positions, head_dim)
+    cos = torch.from_numpy(cos_b.view(np.int16)).view(torch.bfloat16)
+    sin = torch.from_numpy(sin_b.view(np.int16)).view(torch.bfloat16)
+    rows = [slice(int(cu[b]), int(cu[b + 1])) for b in range(len(lengths))]
+    results = []
+    for order in ([0, 1, 2, 3], [3, 0, 1, 2]):
+        pick = lambda t: torch.cat([t[rows[b]] for b in order]).to(device)
+        ocu = torch.tensor(np.concatenate([[0], np.cumsum([lengths[b] for b in order])]),
+                           dtype=torch.int32, device=device)
+        ak = torch.zeros(4, kv_heads, capacity, head_dim, device=device, dtype=torch.bfloat16)
+        av = torch.zeros_like(ak)
+        out = pkg.prefill_step(pick(q), pick(k), pick(v), pick(cos), pick(sin), ocu, max(lengths), ak, av,
+                               kv_slots=torch.tensor(order, device=device))
+        torch.cuda.synchronize()
+        starts = np.concatenate([[0], np.cumsum([lengths[b] for b in order])])
+        per_prompt = {b: bits(out[int(starts[i]):int(starts[i + 1])]) for i, b in enumerate(order)}
+        results.append((bits(ak), bits(av), per_prompt))
+    (k0, v0, o0), (k1, v1, o1) = results
+    assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
+    for b in range(len(lengths)):
+        assert np.array_equal(o0[b], o1[b]), f"prompt {b}"
+    expected = oatt.prefill_attention(obf16.from_bits(orope.rope_bf16(bits(q), cos_b[:, None, :], sin_b[:, None, :])),
+                                      obf16.from_bits(k0), obf16.from_bits(v0), cu.numpy(), head_dim ** -0.5)
+    got = np.concatenate([obf16.from_bits(o0[b]) for b in range(len(lengths))])
+    assert_attention_close(got, expected)
