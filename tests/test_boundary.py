@@ -122,3 +122,12 @@ def test_packed_prefix_rejects_before_any_write(pkg):
         with pytest.raises(ValueError):
             pkg.copy_packed_prefix(target, bad, 0, length=1)
     assert torch.equal(target, saved)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU; --gpus above 1 exits with a message before touching a GPU."""
+    import sys
+    done = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True,
+                          text=True, timeout=300, cwd=ROOT)
+    assert done.returncode == 2
+    assert "one GPU" in done.stderr and done.stdout == ""
