@@ -58,14 +58,24 @@ def rope_f32(x, cos, sin):
 
 def mrope_select(cos3, sections, interleaved=False):
     """Per-dimension selection of the (3, ...) temporal/height/width tables used by a
-    sectioned multimodal RoPE: consecutive sections [t, h, w] of each half
-    (Qwen2-VL form), or axis f % 3 for frequency f when interleaved.  With three equal
-    axes every selection equals the single-axis table (tests/test_text_rope.py:9-22)."""
+    sectioned multimodal RoPE (packed_attention.py:66-69 calls qwen_tts's
+    apply_multimodal_rotary_pos_emb with the module's mrope_section and interleaved flag).
+
+    * consecutive sections [t, h, w] of each half (the Qwen2-VL form);
+    * interleaved (the Qwen3-Omni talker form): frequency f of each half reads axis
+      a in {1, 2} when f % 3 == a and f < 3 * sections[a], and the temporal axis otherwise,
+      so with [24, 20, 20] the last frequencies 60 ... 63 are temporal.
+
+    With three equal axes every selection equals the single-axis table
+    (tests/test_text_rope.py:9-22)."""
     cos3 = np.asarray(cos3)
     width = cos3.shape[-1]
     half = width // 2
     if interleaved:
-        axis_of = np.array([f % 3 for f in range(half)])
+        axis_of = np.zeros(half, dtype=np.int64)
+        for a in (1, 2):
+            for f in range(a, min(half, 3 * sections[a]), 3):
+                axis_of[f] = a
     else:
         axis_of = np.concatenate([np.full(n, i % 3) for i, n in enumerate(sections)])
     axis_of = np.concatenate([axis_of, axis_of])

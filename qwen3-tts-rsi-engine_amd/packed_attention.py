@@ -77,10 +77,16 @@ def _is_causal_pair(mask, batch):
 
 def _section_axes(head_dim, sections, interleaved, device):
     """Per-dimension axis (0 temporal, 1 height, 2 width) of a sectioned multimodal RoPE:
-    consecutive sections of each half, or frequency f -> f % 3 when interleaved."""
+    consecutive sections of each half, or, interleaved, frequency f reads axis a in {1, 2}
+    when f % 3 == a and f < 3 * sections[a] and the temporal axis otherwise (the Qwen3-Omni
+    talker's layout, which qwen_tts's apply_multimodal_rotary_pos_emb applies at
+    packed_attention.py:66-69)."""
     half = head_dim // 2
     if interleaved:
-        axes = [f % 3 for f in range(half)]
+        axes = [0] * half
+        for a in (1, 2):
+            for f in range(a, min(half, 3 * sections[a]), 3):
+                axes[f] = a
     else:
         axes = [i % 3 for i, n in enumerate(sections) for _ in range(n)]
     if len(axes) != half:

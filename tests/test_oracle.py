@@ -156,10 +156,64 @@ def test_mrope_equal_axes_is_the_text_rope():
     cos3 = np.stack([c, c, c])
     for sections, interleaved in (([24, 20, 20], False), ([16, 24, 24], False), ([24, 20, 20], True)):
         assert np.array_equal(orope.mrope_select(cos3, sections, interleaved), c)
-    # unequal axes: each dimension reads its own axis
-    axes = np.stack([c, c + 1, c + 2])
-    sel = orope.mrope_select(axes, [24, 20, 20])
-    assert np.array_equal(sel[..., :24], c[..., :24]) and np.array_equal(sel[..., 24:44], c[..., 24:44] + 1)
+
+
+def _axis_tables(width=128):
+    """(3, 1, width) tables whose every entry names its own axis and dimension: axis a,
+    dimension d holds 1000 a + d, so a selection shows which axis each dimension read."""
+    d = np.arange(width, dtype=np.float64)
+    return np.stack([1000.0 * a + d for a in range(3)])[:, None, :]
+
+
+def test_mrope_sections_hand_computed():
+    """[24, 20, 20], written out by hand.  Sectioned: dimensions 0-23 temporal, 24-43
+    height, 44-63 width, the same again for 64-127.  Interleaved: frequencies cycle
+    T, H, W from 0 to 59 (3 x 20), and the remaining 60-63 are temporal."""
+    sel = orope.mrope_select(_axis_tables(), [24, 20, 20])[0]
+    axes = (sel // 1000).astype(int)
+    expected_half = [0] * 24 + [1] * 20 + [2] * 20
+    assert axes.tolist() == expected_half + expected_half
+    sel = orope.mrope_select(_axis_tables(), [24, 20, 20], interleaved=True)[0]
+    axes = (sel // 1000).astype(int)
+    expected_half = [0, 1, 2] * 20 + [0, 0, 0, 0]
+    assert axes.tolist() == expected_half + expected_half
+    assert np.array_equal(sel % 1000, np.arange(128))  # every dimension keeps its own column
+    # sections that do not reach the end of the cycle: [32, 16, 16] interleaved gives
+    # T H W for f < 48 and T from 48 to 63
+    axes = (orope.mrope_select(_axis_tables(), [32, 16, 16], interleaved=True)[0] // 1000).astype(int)
+    assert axes[:64].tolist() == [0, 1, 2] * 16 + [0] * 16
+
+
+def test_mrope_matches_transformers_multimodal_rope():
+    """Against the installed transformers' own multimodal RoPE on unequal axes: the
+    interleaved layout of the Qwen3-Omni talker (Qwen3OmniMoeTalkerRotaryEmbedding's
+    apply_interleaved_mrope, acting on the (3, ..., D/2) frequencies before the
+    [f, f] concatenation) and the sectioned layout of Qwen2.5-Omni's
+    apply_multimodal_rotary_pos_emb."""
+    omni3 = pytest.importorskip('transformers.models.qwen3_omni_moe.modeling_qwen3_omni_moe')
+    omni25 = pytest.importorskip('transformers.models.qwen2_5_omni.modeling_qwen2_5_omni')
+    inv = torch.from_numpy(orope.inv_freq(128))
+    gen = torch.Generator().manual_seed(3)
+    pos = torch.randint(0, 4000, (3, 2, 5), generator=gen)          # distinct T, H, W positions
+    freqs = (pos[..., None].double() * inv.double()).float()          # (3, B, S, 64)
+    for sections in ([24, 20, 20], [16, 24, 24]):
+        cat = torch.cat([freqs, freqs], dim=-1)
+        ours = orope.mrope_select(cat.numpy(), sections, interleaved=True)
+        theirs = omni3.Qwen3OmniMoeTalkerRotaryEmbedding.apply_interleaved_mrope(
+            None, freqs.clone(), sections)
+        assert np.array_equal(ours, torch.cat([theirs, theirs], dim=-1).numpy())
+        # sectioned: their function applies the selected tables to q and k; with q = 1 on one
+        # dimension and 0 elsewhere, q * cos + rotate_half(q) * sin reads back cos
+        cos = torch.cos(cat)
+        sin = torch.sin(cat)
+        picked = orope.mrope_select(cos.numpy(), sections)
+        for d in (0, 23, 24, 43, 44, 63, 64, 100, 127):
+            unit = torch.zeros(2, 1, 5, 128, dtype=torch.float32)
+            unit[..., d] = 1.0
+            q_embed, _ = omni25.apply_multimodal_rotary_pos_emb(unit, unit, cos.float(), sin.float(),
+                                                                list(sections))
+            got = q_embed[:, 0, :, d].numpy()
+            assert np.array_equal(got, picked[..., d].astype(np.float32)), (sections, d)
 
 
 # ---- attention ---------------------------------------------------------------------------
@@ -411,3 +465,44 @@ def test_rms_norm_closed_forms():
     assert np.array_equal(onorm.rms_norm_bf16(x, w, 0.0), onorm.rms_norm_bf16(x4, w, 0.0))
     zero = np.zeros((1, 128), dtype=np.uint16)
     assert np.all(obf16.from_bits(onorm.rms_norm_bf16(zero, w, 1e-6)) == 0)
+
+
+# ---- the torch CPU path (the timed baseline) against the numpy oracle --------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_torch_path_matches_numpy_oracle_on_config1(dtype):
+    """oracle/torch_path.decode_layer (the reference's eager RoPE, scatter_ write and SDPA
+    under the 0 / finfo.min mask, the CPU baseline's arithmetic) and the numpy restatement
+    (rope + kv_write + decode_attention) agree on the 4-request inputs, contexts
+    {37, 120, 5, 256}: the arena after the write bit for bit, the outputs to 1e-5 in fp32
+    and to the bf16 attention bar in bf16."""
+    from oracle import torch_path
+    from tests.golden.make_golden import CONFIG1_CONTEXTS, config1_inputs
+    cache_k, cache_v, q, k, v = (t.to(dtype) for t in config1_inputs())
+    positions = torch.tensor(CONFIG1_CONTEXTS, dtype=torch.int64)
+    inv = torch.from_numpy(orope.inv_freq(128))
+    angle = positions[:, None].float() * inv[None, :]
+    emb = torch.cat([angle, angle], dim=-1)
+    cos, sin = emb.cos().to(dtype)[:, None], emb.sin().to(dtype)[:, None]      # (B, 1, D)
+
+    arena_k, arena_v = cache_k.clone(), cache_v.clone()
+    out = torch_path.decode_layer(q, k, v, cos, sin, arena_k, arena_v, positions)
+
+    if dtype == torch.float32:
+        qr = orope.rope_f32(q.numpy(), cos.numpy()[:, :, None], sin.numpy()[:, :, None])
+        kr = orope.rope_f32(k.numpy(), cos.numpy()[:, :, None], sin.numpy()[:, :, None])
+        ok_, ov_ = cache_k.numpy().copy(), cache_v.numpy().copy()
+        okv.kv_write(ok_, ov_, kr.transpose(0, 2, 1, 3), v.numpy().transpose(0, 2, 1, 3), positions.numpy())
+        assert np.array_equal(arena_k.numpy(), ok_) and np.array_equal(arena_v.numpy(), ov_)
+        ref = oatt.decode_attention(qr, ok_, ov_, positions.numpy(), 128 ** -0.5)
+        assert np.abs(out.double().numpy() - ref).max() <= 1e-5
+    else:
+        qr = orope.rope_bf16(_torch_bits(q), _torch_bits(cos)[:, :, None], _torch_bits(sin)[:, :, None])
+        kr = orope.rope_bf16(_torch_bits(k), _torch_bits(cos)[:, :, None], _torch_bits(sin)[:, :, None])
+        ok_, ov_ = _torch_bits(cache_k).copy(), _torch_bits(cache_v).copy()
+        okv.kv_write(ok_, ov_, kr.transpose(0, 2, 1, 3), _torch_bits(v).transpose(0, 2, 1, 3), positions.numpy())
+        assert np.array_equal(_torch_bits(arena_k), ok_) and np.array_equal(_torch_bits(arena_v), ov_)
+        ref = oatt.decode_attention(obf16.from_bits(qr), obf16.from_bits(ok_), obf16.from_bits(ov_),
+                                    positions.numpy(), 128 ** -0.5)
+        err = np.abs(out.double().numpy() - ref)
+        assert err.max() <= 2e-2 and err.mean() <= 2e-3

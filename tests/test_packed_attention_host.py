@@ -1,7 +1,10 @@
 """Host-side routing of PackedAttention on the CPU: which predictor first-step masks count as
 the 2x2 causal mask (continuous.py:39-40: zeros with finfo.min above the diagonal; no mask
 means causal for two queries, npu_attention.py:17-18), and the bounded cache of results."""
+import numpy as np
 import torch
+
+from oracle import rope as orope
 
 from qwen3_tts_engine_amd import packed_attention as pa
 
@@ -44,3 +47,14 @@ def test_results_follow_in_place_changes_and_the_cache_is_bounded():
     for i in range(3 * pa._CAUSAL_PAIR_LIMIT):
         pa._is_causal_pair(causal_mask(torch.float32) * (1 + i % 2), 4)
     assert len(pa._CAUSAL_PAIR) <= pa._CAUSAL_PAIR_LIMIT
+
+
+def test_section_axes_follow_the_oracle_selection():
+    """The per-dimension axis table PackedAttention gathers with equals the oracle's
+    sectioned and interleaved selections (pinned by hand and against transformers)."""
+    tables = np.stack([1000.0 * a + np.arange(128.0) for a in range(3)])[:, None, :]
+    for sections in ([24, 20, 20], [16, 24, 24], [32, 16, 16]):
+        for interleaved in (False, True):
+            axes = pa._section_axes(128, sections, interleaved, 'cpu').numpy()
+            expected = (orope.mrope_select(tables, sections, interleaved)[0] // 1000).astype(int)
+            assert axes.tolist() == expected.tolist()
