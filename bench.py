@@ -366,7 +366,10 @@ def main():
     parser.add_argument("--steps", type=int, default=200)
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--max-chunks", type=int, default=0,
-                        help="64-key chunks (workgroups) per request and KV head (0 = default)")
+                        help="chunked grid: 64-key chunks per request and KV head (0 = default)")
+    parser.add_argument("--splits", type=int, default=0,
+                        help="decode grid: > 0 balanced with this many workgroups per KV head, "
+                             "< 0 chunked, 0 automatic (balanced for the talker arena)")
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--calibrate-bytes", type=int, default=0,
@@ -410,7 +413,8 @@ def main():
 
     def step():
         for q, k, v, ak, av, o in views:
-            pkg.decode_step(q, k, v, ak, av, positions, cos, sin, out=o, max_chunks=args.max_chunks)
+            pkg.decode_step(q, k, v, ak, av, positions, cos, sin, out=o, max_chunks=args.max_chunks,
+                            splits=args.splits)
 
     step()  # eager: sizes the workspace before capture
     torch.cuda.synchronize()
@@ -439,12 +443,13 @@ def main():
     # attention alone: the non-fused kernel over the already-written arena, same graph method
     q0 = views[0][0].contiguous()
     attn_graph = torch.cuda.CUDAGraph()
-    pkg.decode_attention(q0, arena[0], arena[LAYERS], positions, max_chunks=args.max_chunks)
+    pkg.decode_attention(q0, arena[0], arena[LAYERS], positions, max_chunks=args.max_chunks,
+                         splits=args.splits)
     torch.cuda.synchronize()
     with torch.cuda.graph(attn_graph):
         for layer in range(LAYERS):
             pkg.decode_attention(q0, arena[layer], arena[LAYERS + layer], positions,
-                                 out=out[layer], max_chunks=args.max_chunks)
+                                 out=out[layer], max_chunks=args.max_chunks, splits=args.splits)
     attn_graph.replay()
     torch.cuda.synchronize()
     reps = max(1, args.steps // 4)
@@ -496,12 +501,14 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS,
                      "traffic": traffic},
-        "detail": {"kernel": "decode_attention_kernel<bf16,128,G2,SQ1,fused,streamed>",
+        "detail": {"kernel": ("decode_chunks_kernel" if args.splits < 0 else "decode_balanced_kernel")
+                             + "<bf16,128,G2,SQ1,fused,streamed>",
                    "algorithmic_bytes_per_launch": bytes_per_launch,
                    "us_per_layer_launch": launch_us,
                    "us_per_layer_attention_only": attn_us,
                    "attention_only_GBs": attention_bytes(contexts) / (attn_us * 1e-6) / 1e9,
                    "max_chunks": args.max_chunks,
+                   "splits": args.splits,
                    "wall_s_timed_region": wall,
                    **extra},
     }

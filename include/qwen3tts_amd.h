@@ -119,10 +119,14 @@ int q3t_rope_tables(const int64_t *positions, int64_t n, const float *inv_freq, 
  * as SDPA does (bool masks: nonzero attends).  Requests with p_b outside [0, ctx) attend
  * nothing and get zero rows.  Query head hq reads KV head hq / (q_heads / kv_heads).
  *
- * Keys are cut into chunks of 64 consecutive keys (runs of several such blocks when a
- * request has more than `max_chunks` blocks); every (request, chunk, KV head) is one
- * workgroup; chunks past a request's length exit at once.  A request with several chunks merges the chunks' partial softmax states
- * through `workspace`; the last chunk to finish writes the output.
+ * Two grids compute the same result.  The balanced grid (`splits` workgroups per KV head)
+ * cuts the concatenated keys of all requests of a head into equal shares, one per
+ * workgroup, so that ragged lengths keep every workgroup equally busy; it is the default
+ * for long contexts (ctx >= 2048).  The chunked grid cuts each request's keys into chunks
+ * of 64-key blocks (at most `max_chunks` per request), one workgroup per (request, chunk,
+ * KV head); it is the default for shorter contexts (the talker's 1024-row arena, the code
+ * predictor's 16-row caches).  A request covered by several workgroups merges their partial
+ * softmax states through `workspace`; the last workgroup to finish writes the output.
  *
  * fused != 0 additionally performs, for query_len S in {1, 2} (the step's tokens sit at
  * positions p_b - S + 1 ... p_b):
@@ -166,12 +170,12 @@ typedef struct q3t_decode_args {
     const void *cos, *sin;
     int64_t cs_stride_b;
     /* workspace: a fixed 256 KiB counter region (kv_heads * batch <= 65536), then the
-       partial states of multi-chunk requests; zero-filled before first use, its counters
-       left zeroed by every launch.  Launches that overlap in time must not share one. */
+       partial states of split requests; zero-filled before first use, its counters left
+       zeroed by every launch.  Launches that overlap in time must not share one. */
     void *workspace;
     int64_t workspace_bytes;
-    int64_t max_chunks;      /* chunks per request and KV head, <= 1024; <= 0: enough for
-                                about 512 workgroups over the batch */
+    int64_t max_chunks;      /* chunked grid: chunks per request and KV head, <= 1024; <= 0:
+                                enough for about 512 workgroups over the batch */
     /* fused only, optional: RMSNorm of the query rows / the new key rows before RoPE (the
        q_norm / k_norm of the attention module, packed_attention.py:42-45):
        bf16(weight * bf16(x * rsqrt(mean(x^2) + norm_eps))) with the fp32 sum of squares of a
@@ -180,16 +184,26 @@ typedef struct q3t_decode_args {
     float norm_eps;
     /* fused, S == 2: token strides of new_key, new_value and cos/sin (elements) */
     int64_t nk_stride_s, nv_stride_s, cs_stride_s;
+    /* grid: > 0 the balanced grid with this many workgroups per KV head (<= 32768; fewer
+       run when the keys are few: at least 32 keys per workgroup); < 0 the chunked grid;
+       0 automatic (balanced with 256 workgroups in all for ctx >= 2048 and for fused steps
+       with a mask; chunked otherwise) */
+    int64_t splits;
 } q3t_decode_args;
 
-/* Bytes of workspace needed by q3t_decode_attention for these sizes.  No counterpart in
-   the reference (its attention operator allocates internally); callers size the buffer
-   once, outside graph capture. */
-int64_t q3t_decode_workspace_bytes(int64_t batch, int64_t query_len, int64_t q_heads,
-                                   int64_t kv_heads, int64_t head_dim, int64_t ctx,
-                                   int64_t max_chunks);
+/* Bytes of workspace q3t_decode_attention needs for this call (its sizes, `fused`, `mask`,
+   `max_chunks` and `splits`; pointers are not read); -1 for malformed sizes.  No
+   counterpart in the reference (its attention operator allocates internally); callers size
+   the buffer once, outside graph capture. */
+int64_t q3t_decode_workspace_bytes(const q3t_decode_args *args);
 
 int q3t_decode_attention(const q3t_decode_args *args, void *stream);
+
+/* Re-zero the counter region of a decode workspace on `stream` (a kernel, so it may be
+   captured).  Every completed launch leaves the counters zeroed; a launch that failed
+   part-way may not, and the next launch that splits a request would then miscount.  No
+   counterpart in the reference (its operator keeps no state between calls). */
+int q3t_decode_reset_workspace(void *workspace, int64_t workspace_bytes, void *stream);
 
 /*
  * Varlen causal prefill attention with GQA on bf16 MFMA tiles.

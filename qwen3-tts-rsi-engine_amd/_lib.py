@@ -48,6 +48,7 @@ class DecodeArgs(ctypes.Structure):
         ("workspace", c_vp), ("workspace_bytes", c_i64), ("max_chunks", c_i64),
         ("q_norm_weight", c_vp), ("k_norm_weight", c_vp), ("norm_eps", ctypes.c_float),
         ("nk_stride_s", c_i64), ("nv_stride_s", c_i64), ("cs_stride_s", c_i64),
+        ("splits", c_i64),
     ]
 
 
@@ -94,8 +95,9 @@ SIGNATURES = {
     "q3t_rotary": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp]),
     "q3t_rope_tables": (ctypes.c_int, [c_vp, c_i64, c_vp, c_i64, ctypes.c_float, c_i64, c_vp,
                                        c_vp, c_vp]),
-    "q3t_decode_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64]),
+    "q3t_decode_workspace_bytes": (c_i64, [ctypes.POINTER(DecodeArgs)]),
     "q3t_decode_attention": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
+    "q3t_decode_reset_workspace": (ctypes.c_int, [c_vp, c_i64, c_vp]),
     "q3t_prefill_attention": (ctypes.c_int, [ctypes.POINTER(PrefillArgs), c_vp]),
     "q3t_prefill_rope_write": (ctypes.c_int, [ctypes.POINTER(PrefillRopeWriteArgs), c_vp]),
 }
@@ -108,7 +110,7 @@ class KernelError(RuntimeError):
     """A HIP launch failed after host validation passed."""
 
 
-ABI_VERSION = 3  # q3t_abi_version() of the header these structures mirror
+ABI_VERSION = 4  # q3t_abi_version() of the header these structures mirror
 
 
 def library() -> ctypes.CDLL:

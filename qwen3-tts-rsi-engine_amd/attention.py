@@ -20,22 +20,51 @@ _WORKSPACES: dict = {}
 _RETIRED: list = []
 
 
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Zero-filled split-K workspace shared by every launch on ``device``.
+class _Workspace:
+    __slots__ = ('buffer', 'captured')
 
-    Kernels leave its counters zeroed, so one buffer serves all sequential launches on a
-    stream.  Launches that overlap on two streams of one device must not share it.
-    It grows only outside graph capture; earlier buffers stay alive for captured graphs."""
-    current = _WORKSPACES.get(device)
-    if current is not None and current.numel() >= nbytes:
-        return current
-    if torch.cuda.is_current_stream_capturing():
-        raise ValueError('decode workspace must be sized by an eager call before graph capture')
-    grown = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-    if current is not None:
-        _RETIRED.append(current)
-    _WORKSPACES[device] = grown
-    return grown
+    def __init__(self, buffer):
+        self.buffer = buffer
+        self.captured = False  # a graph captured a launch that uses this buffer
+
+
+def workspace(device: torch.device, nbytes: int, stream: int | None = None) -> torch.Tensor:
+    """Split-softmax workspace of one stream of ``device``, its counters zeroed.
+
+    Kernels leave the counters zeroed, so one buffer serves every sequential launch on its
+    stream; launches on different streams get different buffers, so they may overlap.  A
+    new buffer's counters are cleared by the library's reset kernel on that stream, which
+    is a kernel node when the stream is being captured (no memset node in a graph), so a
+    buffer can also be created during capture; it then comes from the graph's memory pool.
+    A replaced buffer that some captured graph uses stays alive with the process (the graph
+    may be replayed); one that no graph captured is released at once."""
+    stream = _lib.stream_handle(device) if stream is None else stream
+    key = (device, stream)
+    capturing = torch.cuda.is_current_stream_capturing()
+    current = _WORKSPACES.get(key)
+    if current is None or current.buffer.numel() < nbytes:
+        buffer = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        status = _lib.library().q3t_decode_reset_workspace(buffer.data_ptr(), buffer.numel(), stream)
+        _lib.check(status, 'decode workspace')
+        if current is not None and current.captured:
+            _RETIRED.append(current.buffer)
+        _WORKSPACES[key] = current = _Workspace(buffer)
+    if capturing:
+        current.captured = True
+    return current.buffer
+
+
+def reset_workspaces(device: torch.device | None = None) -> None:
+    """Re-zero the counters of every decode workspace (of ``device``, or of all devices),
+    on each workspace's own stream: after a launch that failed part-way, counters may be
+    left non-zero and would mislead the next launch that splits a request."""
+    lib = _lib.library()
+    for (dev, stream), ws in list(_WORKSPACES.items()):
+        if device is not None and dev != torch.device(device):
+            continue
+        with torch.cuda.device(dev):
+            status = lib.q3t_decode_reset_workspace(ws.buffer.data_ptr(), ws.buffer.numel(), stream)
+        _lib.check(status, 'decode workspace reset')
 
 
 def _mask_view(mask, batch, query_len, ctx):
@@ -56,25 +85,33 @@ def _mask_view(mask, batch, query_len, ctx):
 def _run_decode(args: _lib.DecodeArgs, device: torch.device, what: str) -> None:
     lib = _lib.library()
     with torch.cuda.device(device):
-        need = lib.q3t_decode_workspace_bytes(args.batch, args.query_len, args.q_heads,
-                                              args.kv_heads, args.head_dim, args.ctx,
-                                              args.max_chunks)
+        need = lib.q3t_decode_workspace_bytes(args)
         if need < 0:
             raise ValueError(f'{what}: invalid sizes')
-        ws = workspace(device, need)
+        stream = _lib.stream_handle(device)
+        ws = workspace(device, need, stream)
         args.workspace = ws.data_ptr()
         args.workspace_bytes = ws.numel()
-        status = lib.q3t_decode_attention(args, _lib.stream_handle(device))
+        status = lib.q3t_decode_attention(args, stream)
     _lib.check(status, what)
 
 
+def _check_out(out, shape, dtype, device, what):
+    """A caller-supplied output: the exact shape and dtype, unit-stride rows, on the device."""
+    if (tuple(out.shape) != tuple(shape) or out.dtype != dtype or out.device != device
+            or out.stride(-1) != 1):
+        raise ValueError(f'{what}: out must be a {tuple(shape)} {dtype} tensor on {device} '
+                         'with unit-stride rows')
+
+
 def decode_attention(query, keys, values, positions, *, scale=None, mask=None, kv_offsets=None,
-                     out=None, max_chunks=0):
+                     out=None, max_chunks=0, splits=0):
     """query (B, S, Hq, D) BSND; keys/values (B, Hkv, ctx, D) views of the arena (or, with
     ``kv_offsets``, any base tensor whose request rows start at those element offsets);
-    positions (B,) int64: the last query position of each request.  ``max_chunks`` bounds the
-    64-key chunks (workgroups) per request and KV head (0: the default, 64).
-    Returns (B, S, Hq, D)."""
+    positions (B,) int64: the last query position of each request.  ``splits`` picks the
+    grid: > 0 equal shares of each head's keys over that many workgroups, < 0 chunks of
+    64-key blocks per request (at most ``max_chunks``, 0: enough for ~512 workgroups),
+    0 automatic.  Returns (B, S, Hq, D)."""
     if query.ndim != 4 or keys.ndim != 4 or values.shape != keys.shape:
         raise ValueError('expected BSND query and BNSD key/value views')
     batch, qlen, q_heads, head_dim = query.shape
@@ -93,8 +130,8 @@ def decode_attention(query, keys, values, positions, *, scale=None, mask=None, k
     device = _lib.require_gpu(*tensors)
     if out is None:
         out = torch.empty(batch, qlen, q_heads, head_dim, device=device, dtype=query.dtype)
-    elif out.shape != (batch, qlen, q_heads, head_dim) or out.dtype != query.dtype or out.stride(3) != 1:
-        raise ValueError('out must be (B, S, Hq, D) of the query dtype')
+    else:
+        _check_out(out, (batch, qlen, q_heads, head_dim), query.dtype, device, 'decode attention')
     a = _lib.DecodeArgs()
     a.batch, a.query_len, a.q_heads, a.kv_heads, a.head_dim = batch, qlen, q_heads, kv_heads, head_dim
     a.ctx = ctx
@@ -119,13 +156,14 @@ def decode_attention(query, keys, values, positions, *, scale=None, mask=None, k
     a.out = out.data_ptr()
     a.o_stride_b, a.o_stride_s, a.o_stride_h = out.stride()[:3]
     a.max_chunks = int(max_chunks)
+    a.splits = int(splits)
     _run_decode(a, device, 'decode attention')
     return out
 
 
 def decode_step(query, new_key, new_value, key_arena, value_arena, positions, cos, sin, *,
-                scale=None, out=None, max_chunks=0, q_norm_weight=None, k_norm_weight=None,
-                norm_eps=1e-6):
+                scale=None, out=None, max_chunks=0, splits=0, q_norm_weight=None, k_norm_weight=None,
+                norm_eps=1e-6, mask=None):
     """Fused decode step of a layer for one token, or two (the code predictor's first step).
 
     query (B, S, Hq, D), new_key/new_value (B, S, Hkv, D) with S in {1, 2}: un-rotated bf16
@@ -138,7 +176,12 @@ def decode_step(query, new_key, new_value, key_arena, value_arena, positions, co
     With ``q_norm_weight`` / ``k_norm_weight`` (bf16 (D,)) the query / key rows are first
     RMS-normalised in the kernel (the module's q_norm / k_norm, eps ``norm_eps``): raw
     projection rows go in and no separate norm kernels run.  The fp32 row sums follow the
-    kernel's order, so a result can differ from another implementation's in the last bf16 bit."""
+    kernel's order, so a result can differ from another implementation's in the last bf16 bit.
+
+    ``mask`` (SDPA-style, broadcastable to (B, 1, S, C)) is added to the scores of the keys
+    0 ... positions[b], as the reference's operator applies the mask it is given; without it
+    request b attends exactly those keys (the ``j <= pos[b]`` mask of SlotGraph.compute).
+    ``splits`` / ``max_chunks`` choose the grid as in ``decode_attention``."""
     if (query.ndim != 4 or query.shape[1] not in (1, 2) or new_key.ndim != 4
             or new_key.shape[1] != query.shape[1]):
         raise ValueError('fused decode expects one- or two-token BSND rows')
@@ -167,6 +210,8 @@ def decode_step(query, new_key, new_value, key_arena, value_arena, positions, co
     device = _lib.require_gpu(*tensors, positions)
     if out is None:
         out = torch.empty(batch, tokens, q_heads, head_dim, device=device, dtype=query.dtype)
+    else:
+        _check_out(out, (batch, tokens, q_heads, head_dim), query.dtype, device, 'fused decode step')
     a = _lib.DecodeArgs()
     a.batch, a.query_len, a.q_heads, a.kv_heads, a.head_dim = batch, tokens, q_heads, kv_heads, head_dim
     a.ctx = key_arena.shape[2]
@@ -187,6 +232,12 @@ def decode_step(query, new_key, new_value, key_arena, value_arena, positions, co
     a.cos, a.sin = cos3.data_ptr(), sin3.data_ptr()
     a.cs_stride_b, a.cs_stride_s = cos3.stride(0), cos3.stride(1)
     a.max_chunks = int(max_chunks)
+    a.splits = int(splits)
+    if mask is not None:
+        m = _mask_view(mask.to(device), batch, tokens, a.ctx)
+        a.mask = m.data_ptr()
+        a.mask_dtype = _lib.DTYPE_CODES[m.dtype]
+        a.mask_stride_b, a.mask_stride_s, a.mask_stride_t = m.stride()
     for name, weight in (('q_norm_weight', q_norm_weight), ('k_norm_weight', k_norm_weight)):
         if weight is None:
             continue

@@ -1,4 +1,4 @@
-// Ragged grouped-query decode attention over the slot arena, split along the keys.
+// Ragged grouped-query decode attention over the slot arena.
 //
 // Reference behaviour (InferMatrixLab/qwen3-tts-rsi-engine):
 //   out[b, hq] = softmax(q[b, hq] . K[b, hq/G, :L_b]^T * scale + mask) . V[b, hq/G, :L_b]
@@ -11,24 +11,22 @@
 // two tokens per request (the code predictor's first step, continuous.py:37-40) both are
 // rotated, written at pos[b] - 1 and pos[b], and attended causally.
 //
-// Design (one launch per layer, no per-step preparation):
-//   * keys are cut into chunks of kChunkRows consecutive keys (several consecutive blocks
-//     per chunk when a request has more blocks than `nchunks`); one 256-thread workgroup per
-//     (request, chunk, KV head).  The grid covers nchunks chunks of every request; chunks
-//     past L_b leave at once.  Small independent workgroups let the hardware dispatcher keep
-//     every CU saturated with loads across the ragged lengths, which measured faster than
-//     any persistent per-CU assignment of the same keys.
-//   * blockIdx.x % kv_heads is the KV head, so with 8 KV heads each head maps to one XCD
-//     under the round-robin dispatch, together with its partial states and counters.
+// Design (one launch per layer, no per-step preparation): two grids over the same per-range
+// core (PairWork):
+//   * balanced (arena-sized launches, the talker step): each KV head's keys of all requests
+//     are cut into equal shares, one per workgroup, so ragged lengths do not leave the
+//     longest requests to a few workgroups at the end of the launch; the shares are derived
+//     on the device from the positions;
+//   * chunked (small caches, the code predictor): one workgroup per (request, chunk of 64-key
+//     blocks, KV head), whose rows are requested together with its position.
 //   * lanes: 16 bytes of one key row per lane (LPK lanes per key); a pass of the workgroup
 //     reads 4 KiB of K and 4 KiB of V, all passes of a block are issued before any math;
 //     large arenas are read with the non-temporal cache policy (each row is read once).
 //     Scores are reduced across the LPK lanes with DPP, the softmax max across a wave's lane
 //     groups with permlane swaps, and the waves' (max, sum, acc) states merge in LDS.
-//   * a request with one chunk writes its output directly.  Otherwise every chunk publishes
-//     its state with device-scope stores and bumps a per-(request, head) counter; the last
-//     arriver merges all chunk states in chunk order (deterministic), writes the output
-//     and re-zeroes the counter, so launches can be replayed from a graph.
+//   * a (request, head) covered by several workgroups combines their states through the
+//     workspace (finish_split): the last one to arrive merges in part order, writes the
+//     output and re-zeroes the pair's counter, so launches can be replayed from a graph.
 #include "q3t_common.hpp"
 
 namespace q3t {
@@ -40,9 +38,11 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kEmpty = -1.0e30f;  // finite "no key yet" running max
+constexpr int kMinShare = 32;       // balanced grid: fewest keys per workgroup
 
 struct DecodeParams {
     int B, Hq, Hkv, ctx, nchunks;
+    int splits;             // balanced grid: workgroups per KV head (0: chunked grid)
     float scale_log2;
     int has_mask, mask_dtype;
     const char *q;
@@ -253,60 +253,417 @@ constexpr int decode_waves_per_eu(int es, int rows, bool mask) {
     return es == 2 && rows <= 2 ? (mask ? 5 : 6) : 1;
 }
 
+// The work of one workgroup on one (request, KV head) pair over a key range [j0, j1): the
+// online softmax of the pair's G * SQ query rows, shared by both grids below.
+//   load_rows  requests the rows that depend only on (request, head): the query rows and,
+//              fused, the step's cos/sin rows and new key/value rows (16 bytes per lane
+//              each; lane group t holds token t's new rows).  Callers issue it before the
+//              request's key count is known.
+//   attend     streams the arena keys of the range in 64-key blocks (every pass of a block
+//              issued before any math; with PIPE the next block is requested before the
+//              current one is folded in, which costs a second block of registers), folds in the step's new keys when `finisher`
+//              (fused: rotated, written to the arena at L-SQ ... L-1 and attended from LDS;
+//              no workgroup reads those arena rows in the same launch), and leaves the
+//              range's merged state in wave 0: for output t = lane + 64 i (query row
+//              t / D, dim t % D) the unnormalised accumulator A[i], the weight sum Ls[i]
+//              and the running maximum Mx[i] in scaled log2 units.
+template <typename T, int D, int G, int SQ, bool FUSED, bool MASK, bool STREAM, bool PIPE>
+struct PairWork {
+    static constexpr int R = G * SQ;
+    using S = DecodeShape<T, D>;
+    static constexpr int LPK = S::LPK, CW = S::CW, RPW = S::RPW, RPP = S::RPP, P = S::P, ES = S::ES;
+    static constexpr int OPL = R * D / 64;  // outputs per lane of wave 0
+    static constexpr int HD = D;
+    static_assert(!FUSED || (ES == 2 && D == 128 && SQ <= 2), "fused path: bf16, D=128, one or two tokens");
+
+    struct Lds {
+        float acc[kWaves][R][D];
+        float ml[kWaves][R][2];
+    };
+    using NewRows = U4[2][FUSED ? SQ : 1][16];  // rotated new keys, new values (fused)
+
+    U4 qr[R];
+    U4 nk, nv, cv[SQ], sv[SQ];
+
+    Q3T_DEVICE void load_rows(const DecodeParams &p, int b, int h) {
+        const int lane = threadIdx.x & 63, grp = lane / LPK, cl = lane % LPK;
+        if constexpr (FUSED) {
+#pragma unroll
+            for (int t = 0; t < SQ; ++t) {
+                cv[t] = load16(p.cs + (b * p.cs_sb + t * p.cs_ss) * 2 + cl * 16);
+                sv[t] = load16(p.sn + (b * p.cs_sb + t * p.cs_ss) * 2 + cl * 16);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int qi = r / G, hq = h * G + r % G;
+            qr[r] = load16(p.q + (b * p.q_sb + qi * p.q_ss + hq * p.q_sh) * ES + cl * 16);
+        }
+        if constexpr (FUSED) {
+            const int tk = grp < SQ ? grp : SQ - 1;
+            nk = load16(p.nk + (b * p.nk_sb + tk * p.nk_ss + h * p.nk_sh) * ES + cl * 16);
+            nv = load16(p.nv + (b * p.nv_sb + tk * p.nv_ss + h * p.nv_sh) * ES + cl * 16);
+        }
+    }
+
+    // Zero output rows of a request without a valid position (it attends nothing).
+    static Q3T_DEVICE void write_zeros(const DecodeParams &p, int b, int h) {
+        for (int t = threadIdx.x; t < R * D; t += kThreads) {
+            const int r = t / D, d = t % D, qi = r / G, hq = h * G + r % G;
+            store_out<T>(p.out + (b * p.o_sb + qi * p.o_ss + hq * p.o_sh + d) * ES, 0.f);
+        }
+    }
+
+    // Wave 0: final output rows A / Ls of request b.
+    static Q3T_DEVICE void write_out(const DecodeParams &p, int b, int h, const float (&A)[OPL],
+                                     const float (&Ls)[OPL]) {
+        const int lane = threadIdx.x & 63;
+#pragma unroll
+        for (int i = 0; i < OPL; ++i) {
+            const int t = lane + 64 * i, r = t / D, d = t % D, qi = r / G, hq = h * G + r % G;
+            store_out<T>(p.out + (b * p.o_sb + qi * p.o_ss + hq * p.o_sh + d) * ES,
+                         A[i] * __builtin_amdgcn_rcpf(Ls[i]));
+        }
+    }
+
+    Q3T_DEVICE void attend(const DecodeParams &p, int b, int h, int L, int j0, int j1, bool finisher,
+                           Lds &lds, NewRows &snew, float (&A)[OPL], float (&Ls)[OPL], float (&Mx)[OPL]) {
+        const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+        const int grp = lane / LPK, cl = lane % LPK;
+        const bool with_new = FUSED && finisher;
+        const int jend = FUSED ? min(j1, L - SQ) : j1;  // arena keys of the range: [j0, jend)
+
+        const char *kb = p.k + ((p.offs ? p.offs[b] : (int64_t)b * p.k_sb) + h * p.k_sh) * ES;
+        const char *vb = p.v + ((p.offs ? p.offs[b] : (int64_t)b * p.v_sb) + h * p.v_sh) * ES;
+        const int kst = (int)(p.k_st * ES), vst = (int)(p.v_st * ES);
+        const bool same_stride = kst == vst;
+        // K/V rows 0 .. ctx-1 of (b, h) through buffer resources (32-bit row offsets)
+        const auto krs = buffer_rsrc(uniform_ptr(kb), (uint32_t)((p.ctx - 1) * kst + D * ES));
+        const auto vrs = buffer_rsrc(uniform_ptr(vb), (uint32_t)((p.ctx - 1) * vst + D * ES));
+        const char *mask_row = MASK ? p.mask + b * p.m_sb * mask_elem_size(p.mask_dtype) : nullptr;
+
+        // keys of the block at jb: rows at or past jend get an offset outside the resource,
+        // which reads zeros without a memory access
+        auto load_block = [&](int jb, U4 (&kr)[P], U4 (&vr)[P]) {
+#pragma unroll
+            for (int pp = 0; pp < P; ++pp) {
+                const int j = jb + pp * RPP + wave * RPW + grp;
+                const bool ok = j < jend;
+                const uint32_t ko = ok ? (uint32_t)(j * kst) + cl * 16 : 0xfffffff0u;
+                const uint32_t vo = ok ? (same_stride ? ko : (uint32_t)(j * vst) + cl * 16) : 0xfffffff0u;
+                if constexpr (STREAM) {
+                    kr[pp] = buffer_load16_stream(krs, ko);
+                    vr[pp] = buffer_load16_stream(vrs, vo);
+                } else {
+                    kr[pp] = buffer_load16(krs, ko);
+                    vr[pp] = buffer_load16(vrs, vo);
+                }
+            }
+        };
+
+        // with PIPE the first block is requested before the query prologue and every later
+        // block while the one before it is being folded in; without, each block after the
+        // previous one (fewer registers: the chunked grid's rows arrive with the position)
+        U4 kr[PIPE ? P : 1], vr[PIPE ? P : 1];
+        if constexpr (PIPE) load_block(j0, kr, vr);
+
+        U4 q[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) q[r] = qr[r];
+        if constexpr (FUSED) {
+            if (p.qnw) {
+                const U4 w = load16(p.qnw + cl * 16);
+#pragma unroll
+                for (int r = 0; r < R; ++r) q[r] = rms_norm8<LPK>(q[r], w, p.eps, D);
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) q[r] = rope_half8(q[r], xor8_u4(q[r]), cv[r / G], sv[r / G], cl < 8);
+            if (with_new && wave == 0 && grp < SQ && L - SQ + grp >= 0) {
+                // lane group t of wave 0 holds token t's whole rows, so the half exchange (and
+                // the norm's row sum) sees every element
+                const U4 ct = SQ == 1 || grp == 0 ? cv[0] : cv[SQ - 1];
+                const U4 st = SQ == 1 || grp == 0 ? sv[0] : sv[SQ - 1];
+                U4 kx = nk;
+                if (p.knw) kx = rms_norm8<LPK>(nk, load16(p.knw + cl * 16), p.eps, D);
+                const U4 kn = rope_half8(kx, xor8_u4(kx), ct, st, cl < 8);
+                const int row = L - SQ + grp;
+                buffer_store16(krs, (uint32_t)(row * kst) + cl * 16, kn);
+                buffer_store16(vrs, (uint32_t)(row * vst) + cl * 16, nv);
+                snew[0][grp][cl] = kn;
+                snew[1][grp][cl] = nv;
+            }
+        }
+
+
+        float m[R], l[R], acc[R][CW];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            m[r] = kEmpty;
+            l[r] = 0.f;
+#pragma unroll
+            for (int e = 0; e < CW; ++e) acc[r][e] = 0.f;
+        }
+
+        // one online-softmax step over P key vectors per lane (invalid ones carry -inf scores)
+        auto step = [&](const U4 (&kr)[P], const U4 (&vr)[P], const int (&kidx)[P], const bool (&valid)[P],
+                        const float (&mk)[P][SQ], bool rescale) {
+            float s[P][R];
+#pragma unroll
+            for (int pp = 0; pp < P; ++pp)
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int qi = r / G;
+                    bool ok = valid[pp];
+                    // several queries of a request without a mask: causal among the last keys
+                    if constexpr (SQ > 1 && !MASK) ok = ok && kidx[pp] <= L - SQ + qi;
+                    float x = group_sum<LPK>(lane_dot<T>(q[r], kr[pp])) * p.scale_log2;
+                    if constexpr (MASK) x += mk[pp][qi];
+                    s[pp][r] = ok ? x : -INFINITY;
+                }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float mb = s[0][r];
+#pragma unroll
+                for (int pp = 1; pp < P; ++pp) mb = fmaxf(mb, s[pp][r]);
+                const float mn = fmaxf(m[r], cross_max<LPK>(mb));
+                if (rescale) {  // nothing to rescale before the first block
+                    const float alpha = fexp2(m[r] - mn);
+                    l[r] *= alpha;
+#pragma unroll
+                    for (int e = 0; e < CW; ++e) acc[r][e] *= alpha;
+                }
+                m[r] = mn;
+#pragma unroll
+                for (int pp = 0; pp < P; ++pp) {
+                    const float w = fexp2(s[pp][r] - mn);
+                    l[r] += w;
+                    const uint32_t x[4] = {vr[pp].x, vr[pp].y, vr[pp].z, vr[pp].w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if constexpr (ES == 2) {
+                            acc[r][2 * i] += w * bf16_lo(x[i]);
+                            acc[r][2 * i + 1] += w * bf16_hi(x[i]);
+                        } else {
+                            acc[r][i] += w * __uint_as_float(x[i]);
+                        }
+                    }
+                }
+            }
+        };
+
+        // mask terms of keys (log2 units), requested right after the block's key and value
+        // rows so that the scores wait for one round trip, not two
+        auto key_mask = [&](const int (&kidx)[P], const bool (&valid)[P], float (&mk)[P][SQ]) {
+#pragma unroll
+            for (int pp = 0; pp < P; ++pp)
+#pragma unroll
+                for (int qi = 0; qi < SQ; ++qi) {
+                    mk[pp][qi] = 0.f;
+                    if constexpr (MASK) {
+                        if (valid[pp])
+                            mk[pp][qi] = load_mask(mask_row + (qi * p.m_ss + (int64_t)kidx[pp] * p.m_st) *
+                                                                  mask_elem_size(p.mask_dtype),
+                                                   p.mask_dtype) * kLog2e;
+                    }
+                }
+        };
+        auto block_keys = [&](int jb, int (&kidx)[P], bool (&valid)[P]) {
+#pragma unroll
+            for (int pp = 0; pp < P; ++pp) {
+                kidx[pp] = jb + pp * RPP + wave * RPW + grp;
+                valid[pp] = kidx[pp] < jend;
+            }
+        };
+        if constexpr (PIPE) {
+            // two register buffers in turn (the loop handles two blocks per trip, so neither
+            // buffer is ever copied): while one block is folded in, the next one is in flight.
+            // The next block is requested unconditionally (rows past the range read zeros from
+            // outside the buffer resource, without a memory access), so the number of loads in
+            // flight is the same on every path and each block waits only for its own loads.
+            U4 kb2[P], vb2[P];
+            for (int jb = j0; jb < jend; jb += 2 * kChunkRows) {
+                int kidx[P];
+                bool valid[P];
+                float mk[P][SQ];
+                const int j2 = jb + kChunkRows;
+                load_block(j2, kb2, vb2);
+                block_keys(jb, kidx, valid);
+                key_mask(kidx, valid, mk);
+                step(kr, vr, kidx, valid, mk, jb != j0);
+                if (j2 >= jend) break;
+                load_block(j2 + kChunkRows, kr, vr);
+                block_keys(j2, kidx, valid);
+                key_mask(kidx, valid, mk);
+                step(kb2, vb2, kidx, valid, mk, true);
+            }
+        } else {
+            for (int jb = j0; jb < jend; jb += kChunkRows) {
+                U4 kb_[P], vb_[P];
+                int kidx[P];
+                bool valid[P];
+                float mk[P][SQ];
+                load_block(jb, kb_, vb_);
+                block_keys(jb, kidx, valid);
+                key_mask(kidx, valid, mk);
+                step(kb_, vb_, kidx, valid, mk, jb != j0);
+            }
+        }
+        if constexpr (FUSED) {
+            if (with_new && wave == 0) {  // the new keys: token t's in lane group t of wave 0
+                U4 kr[P], vr[P];
+                int kidx[P];
+                bool valid[P];
+                float mk[P][SQ];
+                const U4 zero = {0u, 0u, 0u, 0u};
+                const bool mine = grp < SQ && L - SQ + grp >= 0;
+#pragma unroll
+                for (int pp = 0; pp < P; ++pp) {
+                    kr[pp] = (pp == 0 && mine) ? snew[0][grp < SQ ? grp : 0][cl] : zero;
+                    vr[pp] = (pp == 0 && mine) ? snew[1][grp < SQ ? grp : 0][cl] : zero;
+                    kidx[pp] = L - SQ + grp;
+                    valid[pp] = pp == 0 && mine;
+                }
+                key_mask(kidx, valid, mk);
+                step(kr, vr, kidx, valid, mk, j0 < jend);
+            }
+        }
+
+        // the wave's state: sums across its lane groups, then into LDS
+#pragma unroll
+        for (int r = 0; r < R; ++r) l[r] = cross_sum<LPK>(l[r]);
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                lds.ml[wave][r][0] = m[r];
+                lds.ml[wave][r][1] = l[r];
+            }
+        }
+        store_wave_acc<LPK, CW, R, D>(acc, lds.acc[wave], lane);
+        __syncthreads();
+        if (wave != 0) return;
+#pragma unroll
+        for (int i = 0; i < OPL; ++i) {
+            const int t = lane + 64 * i, r = t / D, d = t % D;
+            float mx = lds.ml[0][r][0];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, lds.ml[w][r][0]);
+            float sl = 0.f, sa = 0.f;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                const float wt = fexp2(lds.ml[w][r][0] - mx);
+                sl += lds.ml[w][r][1] * wt;
+                sa += lds.acc[w][r][d] * wt;
+            }
+            A[i] = sa;
+            Ls[i] = sl;
+            Mx[i] = mx;
+        }
+    }
+};
+
+// A (request, head) pair split over n workgroups: this one holds part k in registers (wave 0).
+// One counter word per pair counts arrivals (low 16 bits) and published states (high 16
+// bits).  A workgroup that is not the last to arrive publishes its state with device-scope
+// stores, waits for them to complete and then counts itself published; the last arriver does
+// not publish: it waits until every other part is published (those workgroups have arrived,
+// so they are running and finish publishing without waiting on anything), merges the parts in
+// part order with its own from registers (the same order whichever part arrives last), writes
+// the output and zeroes the counter for the next launch (no memset node in a graph).  A
+// published wait longer than kSpinLimit polls (never expected) gives NaN rows rather than a
+// hang.
+constexpr int kSpinLimit = 1 << 22;
+
+template <typename Work, typename PartAt>
+Q3T_DEVICE void finish_split(const DecodeParams &p, int b, int h, int n, int k, float *mine,
+                             PartAt part_at, float (&A)[Work::OPL], float (&Ls)[Work::OPL],
+                             float (&Mx)[Work::OPL]) {
+    constexpr int OPL = Work::OPL, DD = Work::HD;
+    const int lane = threadIdx.x & 63;
+    int *counter = p.counters + b * p.Hkv + h;
+    int old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if ((old & 0xffff) != n - 1) {
+#pragma unroll
+        for (int i = 0; i < OPL; ++i) {
+            const int t = lane + 64 * i, r = t / DD, d = t % DD;
+            publish(mine + r * (DD + 2) + d, A[i]);
+            if (d == 0) {
+                publish(mine + r * (DD + 2) + DD, Mx[i]);
+                publish(mine + r * (DD + 2) + DD + 1, Ls[i]);
+            }
+        }
+        wait_stores();
+        if (lane == 0) __hip_atomic_fetch_add(counter, 1 << 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    int ready = old >> 16;
+    bool failed = false;
+    for (int tries = 0; ready < n - 1; ++tries) {
+        if (tries >= kSpinLimit) {
+            failed = true;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        int v = 0;
+        if (lane == 0) v = __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ready = __builtin_amdgcn_readfirstlane(v) >> 16;
+    }
+    float a[OPL], s[OPL], mm[OPL];
+#pragma unroll
+    for (int i = 0; i < OPL; ++i) {
+        a[i] = 0.f;
+        s[i] = 0.f;
+        mm[i] = kEmpty;
+    }
+    for (int kk = 0; kk < n; ++kk) {
+        const float *st = kk == k ? nullptr : part_at(kk);
+#pragma unroll
+        for (int i = 0; i < OPL; ++i) {
+            const int t = lane + 64 * i, r = t / DD, d = t % DD;
+            float ak = A[i], lk = Ls[i], mk = Mx[i];
+            if (st) {
+                mk = collect(st + r * (DD + 2) + DD);
+                lk = collect(st + r * (DD + 2) + DD + 1);
+                ak = collect(st + r * (DD + 2) + d);
+            }
+            const float mn = fmaxf(mm[i], mk);
+            const float wo = fexp2(mm[i] - mn), wk = fexp2(mk - mn);
+            s[i] = s[i] * wo + lk * wk;
+            a[i] = a[i] * wo + ak * wk;
+            mm[i] = mn;
+        }
+    }
+    if (failed) {
+#pragma unroll
+        for (int i = 0; i < OPL; ++i) a[i] = __builtin_nanf("");
+    }
+    Work::write_out(p, b, h, a, s);
+    if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---- chunked grid: one workgroup per (request, chunk, KV head) ------------------------
+// For short contexts (the code predictor's 16-row caches): every pair's rows are requested
+// together with its position, so a workgroup's whole life is two memory round trips.
 template <typename T, int D, int G, int SQ, bool FUSED, bool MASK, bool STREAM>
 __global__ void __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(decode_waves_per_eu(sizeof(T), G * SQ, MASK))))
-decode_attention_kernel(DecodeParams p) {
-    constexpr int R = G * SQ;
-    using S = DecodeShape<T, D>;
-    constexpr int LPK = S::LPK, CW = S::CW, RPW = S::RPW, RPP = S::RPP, P = S::P, ES = S::ES;
-    static_assert(!FUSED || (ES == 2 && D == 128 && SQ <= 2), "fused path: bf16, D=128, one or two tokens");
+decode_chunks_kernel(DecodeParams p) {
+    using Work = PairWork<T, D, G, SQ, FUSED, MASK, STREAM, false>;
+    constexpr int OPL = Work::OPL, R = Work::R;
+    __shared__ typename Work::Lds lds;
+    __shared__ typename Work::NewRows snew;
 
-    __shared__ float sm_acc[kWaves][R][D];
-    __shared__ float sm_ml[kWaves][R][2];
-    __shared__ U4 sm_new[FUSED ? 2 : 1][FUSED ? SQ : 1][16];  // rotated new keys, new values
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int grp = lane / LPK, cl = lane % LPK;
     const int h = blockIdx.x % p.Hkv;
     const int rest = blockIdx.x / p.Hkv;
     const int c = rest % p.nchunks, b = rest / p.nchunks;
 
-    // what depends only on (request, head) is requested together with the position: the query
-    // rows and, fused, the cos/sin rows of the step's tokens and the new key/value rows (16
-    // bytes per lane each; lane group t holds token t's new rows)
     const int64_t pb = p.pos[b];
-    U4 qr[R];
-    U4 nk, nv, cv[SQ], sv[SQ];
-    if constexpr (FUSED) {
-#pragma unroll
-        for (int t = 0; t < SQ; ++t) {
-            cv[t] = load16(p.cs + (b * p.cs_sb + t * p.cs_ss) * 2 + cl * 16);
-            sv[t] = load16(p.sn + (b * p.cs_sb + t * p.cs_ss) * 2 + cl * 16);
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int qi = r / G, hq = h * G + r % G;
-            qr[r] = load16(p.q + (b * p.q_sb + qi * p.q_ss + hq * p.q_sh) * ES + cl * 16);
-        }
-        const int tk = grp < SQ ? grp : SQ - 1;
-        nk = load16(p.nk + (b * p.nk_sb + tk * p.nk_ss + h * p.nk_sh) * ES + cl * 16);
-        nv = load16(p.nv + (b * p.nv_sb + tk * p.nv_ss + h * p.nv_sh) * ES + cl * 16);
-    } else {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int qi = r / G, hq = h * G + r % G;
-            qr[r] = load16(p.q + (b * p.q_sb + qi * p.q_ss + hq * p.q_sh) * ES + cl * 16);
-        }
-    }
-
+    Work work;
+    work.load_rows(p, b, h);
     const int L = (pb >= 0 && pb < p.ctx) ? (int)pb + 1 : 0;
     if (L == 0) {  // no valid position: attends nothing, zero rows (written by chunk 0)
-        if (c == 0)
-            for (int t = tid; t < R * D; t += kThreads) {
-                const int r = t / D, d = t % D, qi = r / G, hq = h * G + r % G;
-                store_out<T>(p.out + (b * p.o_sb + qi * p.o_ss + hq * p.o_sh + d) * ES, 0.f);
-            }
+        if (c == 0) Work::write_zeros(p, b, h);
         return;
     }
     const int nblocks = (L + kChunkRows - 1) / kChunkRows;
@@ -315,258 +672,144 @@ decode_attention_kernel(DecodeParams p) {
     if (c >= n) return;
     const int j0 = c * per * kChunkRows;
     const int j1 = min(L, j0 + per * kChunkRows);
-    // fused: keys L-SQ ... L-1 are the step's new keys; the last chunk writes them and attends
-    // them from LDS, no chunk reads them from the arena
-    const bool with_new = FUSED && c == n - 1;
-    const int jend = FUSED ? min(j1, L - SQ) : j1;  // arena keys of this chunk: [j0, jend)
-
-    const char *kb = p.k + ((p.offs ? p.offs[b] : (int64_t)b * p.k_sb) + h * p.k_sh) * ES;
-    const char *vb = p.v + ((p.offs ? p.offs[b] : (int64_t)b * p.v_sb) + h * p.v_sh) * ES;
-    const int kst = (int)(p.k_st * ES), vst = (int)(p.v_st * ES);
-    const bool same_stride = kst == vst;
-    // K/V rows 0 .. ctx-1 of (b, h) through buffer resources (32-bit row offsets)
-    const auto krs = buffer_rsrc(uniform_ptr(kb), (uint32_t)((p.ctx - 1) * kst + D * ES));
-    const auto vrs = buffer_rsrc(uniform_ptr(vb), (uint32_t)((p.ctx - 1) * vst + D * ES));
-
-    if constexpr (FUSED) {
-        if (p.qnw) {
-            const U4 w = load16(p.qnw + cl * 16);
-#pragma unroll
-            for (int r = 0; r < R; ++r) qr[r] = rms_norm8<LPK>(qr[r], w, p.eps, D);
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) qr[r] = rope_half8(qr[r], xor8_u4(qr[r]), cv[r / G], sv[r / G], cl < 8);
-        if (with_new && wave == 0 && grp < SQ && L - SQ + grp >= 0) {
-            // lane group t of wave 0 holds token t's whole rows, so the half exchange (and the
-            // norm's row sum) sees every element
-            const U4 ct = SQ == 1 || grp == 0 ? cv[0] : cv[SQ - 1];
-            const U4 st = SQ == 1 || grp == 0 ? sv[0] : sv[SQ - 1];
-            U4 kx = nk;
-            if (p.knw) kx = rms_norm8<LPK>(nk, load16(p.knw + cl * 16), p.eps, D);
-            const U4 kn = rope_half8(kx, xor8_u4(kx), ct, st, cl < 8);
-            const int row = L - SQ + grp;
-            buffer_store16(krs, (uint32_t)(row * kst) + cl * 16, kn);
-            buffer_store16(vrs, (uint32_t)(row * vst) + cl * 16, nv);
-            sm_new[0][grp][cl] = kn;
-            sm_new[1][grp][cl] = nv;
-        }
-    }
-
-    const char *mask_row = MASK ? p.mask + b * p.m_sb * mask_elem_size(p.mask_dtype) : nullptr;
-
-    float m[R], l[R], acc[R][CW];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        m[r] = kEmpty;
-        l[r] = 0.f;
-#pragma unroll
-        for (int e = 0; e < CW; ++e) acc[r][e] = 0.f;
-    }
-
-    // one online-softmax step over P key vectors per lane (invalid ones carry -inf scores)
-    auto step = [&](const U4 (&kr)[P], const U4 (&vr)[P], const int (&kidx)[P], const bool (&valid)[P],
-                    const float (&mk)[P][SQ], bool rescale) {
-        float s[P][R];
-#pragma unroll
-        for (int pp = 0; pp < P; ++pp)
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int qi = r / G;
-                bool ok = valid[pp];
-                // several queries of a request without a mask: causal among the last keys
-                if constexpr (SQ > 1 && !MASK) ok = ok && kidx[pp] <= L - SQ + qi;
-                float x = group_sum<LPK>(lane_dot<T>(qr[r], kr[pp])) * p.scale_log2;
-                if constexpr (MASK) x += mk[pp][qi];
-                s[pp][r] = ok ? x : -INFINITY;
-            }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float mb = s[0][r];
-#pragma unroll
-            for (int pp = 1; pp < P; ++pp) mb = fmaxf(mb, s[pp][r]);
-            const float mn = fmaxf(m[r], cross_max<LPK>(mb));
-            if (rescale) {  // nothing to rescale before the first block
-                const float alpha = fexp2(m[r] - mn);
-                l[r] *= alpha;
-#pragma unroll
-                for (int e = 0; e < CW; ++e) acc[r][e] *= alpha;
-            }
-            m[r] = mn;
-#pragma unroll
-            for (int pp = 0; pp < P; ++pp) {
-                const float w = fexp2(s[pp][r] - mn);
-                l[r] += w;
-                const uint32_t x[4] = {vr[pp].x, vr[pp].y, vr[pp].z, vr[pp].w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    if constexpr (ES == 2) {
-                        acc[r][2 * i] += w * bf16_lo(x[i]);
-                        acc[r][2 * i + 1] += w * bf16_hi(x[i]);
-                    } else {
-                        acc[r][i] += w * __uint_as_float(x[i]);
-                    }
-                }
-            }
-        }
-    };
-
-    // keys of the block at jb: rows at or past jend get an offset outside the resource, which
-    // reads zeros without a memory access
-    auto load_block = [&](int jb, U4 (&kr)[P], U4 (&vr)[P]) {
-#pragma unroll
-        for (int pp = 0; pp < P; ++pp) {
-            const int j = jb + pp * RPP + wave * RPW + grp;
-            const bool ok = j < jend;
-            const uint32_t ko = ok ? (uint32_t)(j * kst) + cl * 16 : 0xfffffff0u;
-            const uint32_t vo = ok ? (same_stride ? ko : (uint32_t)(j * vst) + cl * 16) : 0xfffffff0u;
-            if constexpr (STREAM) {
-                kr[pp] = buffer_load16_stream(krs, ko);
-                vr[pp] = buffer_load16_stream(vrs, vo);
-            } else {
-                kr[pp] = buffer_load16(krs, ko);
-                vr[pp] = buffer_load16(vrs, vo);
-            }
-        }
-    };
-    auto block_keys = [&](int jb, int (&kidx)[P], bool (&valid)[P]) {
-#pragma unroll
-        for (int pp = 0; pp < P; ++pp) {
-            kidx[pp] = jb + pp * RPP + wave * RPW + grp;
-            valid[pp] = kidx[pp] < jend;
-        }
-    };
-    // mask terms of the block's keys (log2 units), requested right after the block's key and
-    // value rows so that the scores wait for one round trip, not two
-    auto block_mask = [&](const int (&kidx)[P], const bool (&valid)[P], float (&mk)[P][SQ]) {
-#pragma unroll
-        for (int pp = 0; pp < P; ++pp)
-#pragma unroll
-            for (int qi = 0; qi < SQ; ++qi) {
-                mk[pp][qi] = 0.f;
-                if constexpr (MASK) {
-                    if (valid[pp])
-                        mk[pp][qi] = load_mask(mask_row + (qi * p.m_ss + (int64_t)kidx[pp] * p.m_st) *
-                                                              mask_elem_size(p.mask_dtype),
-                                               p.mask_dtype) * kLog2e;
-                }
-            }
-    };
-    for (int jb = j0; jb < jend; jb += kChunkRows) {
-        U4 kr[P], vr[P];
-        int kidx[P];
-        bool valid[P];
-        float mk[P][SQ];
-        load_block(jb, kr, vr);
-        block_keys(jb, kidx, valid);
-        block_mask(kidx, valid, mk);
-        step(kr, vr, kidx, valid, mk, jb != j0);
-    }
-    if constexpr (FUSED) {
-        if (with_new && wave == 0) {  // the new keys: token t's in lane group t of wave 0
-            U4 kr[P], vr[P];
-            int kidx[P];
-            bool valid[P];
-            float mk[P][SQ] = {};
-            const U4 zero = {0u, 0u, 0u, 0u};
-            const bool mine = grp < SQ && L - SQ + grp >= 0;
-#pragma unroll
-            for (int pp = 0; pp < P; ++pp) {
-                kr[pp] = (pp == 0 && mine) ? sm_new[0][grp < SQ ? grp : 0][cl] : zero;
-                vr[pp] = (pp == 0 && mine) ? sm_new[1][grp < SQ ? grp : 0][cl] : zero;
-                kidx[pp] = L - SQ + grp;
-                valid[pp] = pp == 0 && mine;
-            }
-            step(kr, vr, kidx, valid, mk, j0 < jend);
-        }
-    }
-
-    // the wave's state: sums across its lane groups, then into LDS
-#pragma unroll
-    for (int r = 0; r < R; ++r) l[r] = cross_sum<LPK>(l[r]);
-    if (lane == 0) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            sm_ml[wave][r][0] = m[r];
-            sm_ml[wave][r][1] = l[r];
-        }
-    }
-    store_wave_acc<LPK, CW, R, D>(acc, sm_acc[wave], lane);
-    __syncthreads();
-    // from here on one wave finishes the work item; the others leave and free their slots
-    if (wave != 0) return;
-
-    constexpr int OPL = R * D / 64;  // outputs per lane
-    float *part = p.partials + ((int64_t)(b * p.Hkv + h) * p.nchunks) * (R * (D + 2));
-    float A[OPL], Ls[OPL], M[OPL];
-#pragma unroll
-    for (int i = 0; i < OPL; ++i) {
-        const int t = lane + 64 * i, r = t / D, d = t % D;
-        float mx = sm_ml[0][r][0];
-#pragma unroll
-        for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, sm_ml[w][r][0]);
-        float sl = 0.f, sa = 0.f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float wt = fexp2(sm_ml[w][r][0] - mx);
-            sl += sm_ml[w][r][1] * wt;
-            sa += sm_acc[w][r][d] * wt;
-        }
-        A[i] = sa;
-        Ls[i] = sl;
-        M[i] = mx;
-    }
-    auto out_at = [&](int t) {
-        const int r = t / D, d = t % D, qi = r / G, hq = h * G + r % G;
-        return p.out + (b * p.o_sb + qi * p.o_ss + hq * p.o_sh + d) * ES;
-    };
+    float A[OPL], Ls[OPL], Mx[OPL];
+    work.attend(p, b, h, L, j0, j1, c == n - 1, lds, snew, A, Ls, Mx);
+    if ((threadIdx.x >> 6) != 0) return;
     if (n == 1) {
-#pragma unroll
-        for (int i = 0; i < OPL; ++i) store_out<T>(out_at(lane + 64 * i), A[i] * __builtin_amdgcn_rcpf(Ls[i]));
+        Work::write_out(p, b, h, A, Ls);
         return;
     }
-    float *mine = part + (int64_t)c * (R * (D + 2));
-#pragma unroll
-    for (int i = 0; i < OPL; ++i) {
-        const int t = lane + 64 * i, r = t / D, d = t % D;
-        publish(mine + r * (D + 2) + d, A[i]);
-        if (d == 0) {
-            publish(mine + r * (D + 2) + D, M[i]);
-            publish(mine + r * (D + 2) + D + 1, Ls[i]);
-        }
-    }
+    float *part = p.partials + ((int64_t)(b * p.Hkv + h) * p.nchunks) * (R * (D + 2));
+    finish_split<Work>(p, b, h, n, c, part + (int64_t)c * (R * (D + 2)),
+                       [&](int kk) { return part + (int64_t)kk * (R * (D + 2)); }, A, Ls, Mx);
+}
 
-    // count arrivals; the last chunk of (request, head) merges every chunk state in order
-    wait_stores();
-    int *counter = p.counters + b * p.Hkv + h;
-    int last = 0;
-    if (lane == 0)
-        last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n - 1;
-    if (!__builtin_amdgcn_readfirstlane(last)) return;
+// ---- balanced grid: equal shares of each KV head's ragged key space ---------------------
+// The pairs (b, h) of one KV head laid end to end form a key space of W = sum_b w_b keys,
+// w_b = max(L_b, 1) (a request without a valid position keeps one key slot, whose owner
+// writes its zero rows).  Workgroup i of the head's M covers keys [i W / M, (i + 1) W / M):
+// every workgroup streams the same number of keys, whatever the spread of the lengths, so
+// they all finish together instead of leaving the longest requests to a few workgroups at
+// the end of the launch.  A range crosses request boundaries: it is processed as segments,
+// one per request it touches, in key order.  A segment that is a whole request writes its
+// output; the parts of a split request are combined by finish_split.  Parts of a request
+// always sit in consecutive workgroups, and a request's last part is the first segment of
+// its workgroup, so the states that the last arriver waits for were mostly published long
+// before.  The lengths and their prefix sums are computed by every workgroup from the
+// positions (one load round trip, as a single pair's position costs), so the split needs no
+// preparation launch and follows positions rewritten between graph replays.
+// The balanced kernel keeps two blocks of K/V rows in registers per lane (PIPE) and may use
+// the registers of 2 waves per SIMD: the default grid (256 workgroups, one per CU) needs one,
+// and every variant then compiles without spilling.  Measured on contexts up to 4096 rows,
+// 32 workgroups per KV head (one per CU) beat 64-256: the share of each is longer, so the
+// per-segment costs (query rows, the state merge) weigh less.
+constexpr bool kBalancedPipe = true;
+constexpr int balanced_waves_per_eu(int rows) { return rows <= 2 ? 2 : 1; }
+
+template <typename T, int D, int G, int SQ, bool FUSED, bool MASK, bool STREAM>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(balanced_waves_per_eu(G * SQ))))
+decode_balanced_kernel(DecodeParams p) {
+    using Work = PairWork<T, D, G, SQ, FUSED, MASK, STREAM, kBalancedPipe>;
+    constexpr int OPL = Work::OPL, R = Work::R;
+    constexpr int PER = kMaxBatch / kThreads;  // requests per thread at most
+    __shared__ typename Work::Lds lds[2];      // alternate segments: wave 0 may still read one
+    __shared__ typename Work::NewRows snew;
+    __shared__ int sm_pre[kMaxBatch + 1];      // exclusive prefix sums of w_b
+    __shared__ int sm_len[kMaxBatch];          // L_b, 0 without a valid position
+    __shared__ int sm_wave[kWaves];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = blockIdx.x % p.Hkv;
+    const int wi = blockIdx.x / p.Hkv;
+    {
+        const int per = (p.B + kThreads - 1) / kThreads;
+        int w[PER];
+        int total = 0;
 #pragma unroll
-    for (int i = 0; i < OPL; ++i) {
-        M[i] = kEmpty;
-        Ls[i] = 0.f;
-        A[i] = 0.f;
-    }
-    // online merge in chunk order (deterministic whichever chunk arrives last)
-#pragma unroll 2
-    for (int k = 0; k < n; ++k) {
-        const float *st = part + (int64_t)k * (R * (D + 2));
-#pragma unroll
-        for (int i = 0; i < OPL; ++i) {
-            const int t = lane + 64 * i, r = t / D, d = t % D;
-            const float mk = collect(st + r * (D + 2) + D), lk = collect(st + r * (D + 2) + D + 1);
-            const float ak = collect(st + r * (D + 2) + d);
-            const float mn = fmaxf(M[i], mk);
-            const float wo = fexp2(M[i] - mn), wk = fexp2(mk - mn);
-            Ls[i] = Ls[i] * wo + lk * wk;
-            A[i] = A[i] * wo + ak * wk;
-            M[i] = mn;
+        for (int e = 0; e < PER; ++e) {
+            const int b = tid * per + e;
+            w[e] = 0;
+            if (e < per && b < p.B) {
+                const int64_t pb = p.pos[b];
+                const int L = (pb >= 0 && pb < p.ctx) ? (int)pb + 1 : 0;
+                sm_len[b] = L;
+                w[e] = L > 0 ? L : 1;
+            }
+            total += w[e];
         }
-    }
+        int x = total;  // inclusive scan over the wave
 #pragma unroll
-    for (int i = 0; i < OPL; ++i) store_out<T>(out_at(lane + 64 * i), A[i] * __builtin_amdgcn_rcpf(Ls[i]));
-    if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int off = 1; off < 64; off <<= 1) {
+            const int y = __shfl_up(x, off);
+            if (lane >= off) x += y;
+        }
+        if (lane == 63) sm_wave[wave] = x;
+        __syncthreads();
+        int run = x - total;
+        for (int v = 0; v < wave; ++v) run += sm_wave[v];
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            const int b = tid * per + e;
+            if (e < per && b < p.B) {
+                sm_pre[b] = run;
+                run += w[e];
+            }
+        }
+        if (tid == 0) sm_pre[p.B] = sm_wave[0] + sm_wave[1] + sm_wave[2] + sm_wave[3];
+        __syncthreads();
+    }
+    const int W = __builtin_amdgcn_readfirstlane(sm_pre[p.B]);
+    // at most one workgroup per kMinShare keys (and never more than keys): every range is
+    // non-empty, so every part of a split request arrives
+    int M = W / kMinShare;
+    M = M < 1 ? 1 : (M > p.splits ? p.splits : M);
+    if (wi >= M) return;
+    const int s = (int)((int64_t)wi * W / M), e = (int)((int64_t)(wi + 1) * W / M);
+    int b;  // the request holding key s: the last b with sm_pre[b] <= s
+    {
+        int lo = 0, hi = p.B - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (__builtin_amdgcn_readfirstlane(sm_pre[mid]) <= s) lo = mid;
+            else hi = mid - 1;
+        }
+        b = lo;
+    }
+    for (int seg = 0;; ++seg, ++b) {
+        const int pb0 = __builtin_amdgcn_readfirstlane(sm_pre[b]);
+        const int pb1 = __builtin_amdgcn_readfirstlane(sm_pre[b + 1]);
+        const int L = __builtin_amdgcn_readfirstlane(sm_len[b]);
+        const int j0 = max(s, pb0) - pb0, j1 = min(e, pb1) - pb0;
+        const bool whole = j0 == 0 && pb0 + j1 == pb1;
+        const bool last_segment = pb1 >= e;
+        if (L == 0) {  // one key slot, always whole: zero rows
+            Work::write_zeros(p, b, h);
+        } else {
+            Work work;
+            work.load_rows(p, b, h);
+            float A[OPL], Ls[OPL], Mx[OPL];
+            work.attend(p, b, h, L, j0, j1, j1 == L, lds[seg & 1], snew, A, Ls, Mx);
+            if (wave == 0) {
+                if (whole) {
+                    Work::write_out(p, b, h, A, Ls);
+                } else {
+                    // the request's parts: workgroups ia ... iz (the ones holding its first and
+                    // last key); a part's state sits in slot 0 of its workgroup when the request
+                    // is the workgroup's first segment, else in slot 1
+                    const int ia = (int)(((int64_t)(pb0 + 1) * M - 1) / W);
+                    const int iz = (int)(((int64_t)pb1 * M - 1) / W);
+                    auto part_at = [&](int kk) {
+                        const int j = ia + kk;
+                        const int slot = (j > ia || (int)((int64_t)j * W / M) == pb0) ? 0 : 1;
+                        return p.partials + ((int64_t)(h * p.splits + j) * 2 + slot) * (R * (D + 2));
+                    };
+                    float *mine = p.partials + ((int64_t)(h * p.splits + wi) * 2 + (seg == 0 ? 0 : 1)) * (R * (D + 2));
+                    finish_split<Work>(p, b, h, iz - ia + 1, wi - ia, mine, part_at, A, Ls, Mx);
+                }
+            }
+        }
+        if (last_segment) break;
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -577,13 +820,19 @@ decode_attention_kernel(DecodeParams p) {
 constexpr int64_t kMaxCounters = 65536;  // batch * kv_heads
 static int64_t counters_bytes() { return kMaxCounters * 4; }
 
-// Chunks per (request, KV head): ceil(ctx / 64) at most; by default as many as give about
-// kTargetGroups workgroups for the whole batch, two per CU of the MI355X.  Measured over
-// 8 ... 128 requests (contexts U[64, 1024]), this count was the fastest at every batch size:
-// fewer chunks leave small batches without parallelism, more add chunk states to merge
-// and merge chains at the end of the launch (a 64-request batch runs with one chunk, no
-// merge at all).
+// Chunked grid: chunks per (request, KV head): ceil(ctx / 64) at most; by default as many as
+// give about kTargetGroups workgroups for the whole batch, two per CU of the MI355X.
 constexpr int64_t kTargetGroups = 512;
+
+// Balanced grid: workgroups per KV head by default (kBalancedGroups over all heads), and the
+// context length from which it is the automatic choice.  Measured (bf16, 16/8 heads, contexts
+// drawn uniformly): 128 requests over 4096 rows 170 us balanced against 193 us chunked, over
+// 2048 rows 98 against 108; 8 requests over 8192 rows 31 against 35; but 64 requests over
+// 1024 rows (the talker step) 32-34 against 30 us: on short contexts the balanced grid's
+// per-segment costs outweigh the imbalance it removes.
+constexpr int64_t kBalancedGroups = 256;
+constexpr int64_t kBalancedMinCtx = 2048;
+constexpr int64_t kMaxSplits = 32768;  // a pair's arrivals fit the counter's low 16 bits
 
 // K/V rows are read with the non-temporal policy when the launch may read more than
 // kStreamBytes of them: a talker arena layer (64 requests x 1024 rows: 268 MB) is read once
@@ -604,41 +853,70 @@ static int64_t chunk_count(int64_t batch, int64_t kv_heads, int64_t ctx, int64_t
     return blocks < max_chunks ? blocks : max_chunks;
 }
 
+// The grid a call runs on: > 0 balanced with that many workgroups per KV head, 0 chunked.
+static int64_t balanced_splits(const q3t_decode_args *a) {
+    if (a->splits < 0) return 0;
+    if (a->splits > 0) return a->splits;
+    if (a->ctx < kBalancedMinCtx && !(a->fused && a->mask)) return 0;
+    return (kBalancedGroups + a->kv_heads - 1) / a->kv_heads;
+}
+
+static int64_t partial_floats(const q3t_decode_args *a) {
+    const int64_t R = (a->q_heads / a->kv_heads) * a->query_len;
+    const int64_t splits = balanced_splits(a);
+    const int64_t units = splits > 0 ? a->kv_heads * splits * 2
+                                     : a->batch * a->kv_heads * chunk_count(a->batch, a->kv_heads, a->ctx, a->max_chunks);
+    return units * R * (a->head_dim + 2);
+}
+
 }  // namespace q3t
 
 using namespace q3t;
 
-extern "C" int64_t q3t_decode_workspace_bytes(int64_t batch, int64_t query_len, int64_t q_heads,
-                                              int64_t kv_heads, int64_t head_dim, int64_t ctx,
-                                              int64_t max_chunks) {
-    if (batch < 0 || batch > kMaxBatch || query_len < 1 || kv_heads < 1 || q_heads < kv_heads ||
-        head_dim < 1 || ctx < 1 || ctx > (1 << 20) || max_chunks > kMaxChunks)
-        return -1;
-    const int64_t R = (q_heads / kv_heads) * query_len;
-    return counters_bytes() + batch * kv_heads * chunk_count(batch, kv_heads, ctx, max_chunks) * R * (head_dim + 2) * 4;
+static bool decode_sizes_ok(const q3t_decode_args *a) {
+    return a->batch >= 0 && a->batch <= kMaxBatch && a->query_len >= 1 && a->q_heads >= 1 &&
+           a->kv_heads >= 1 && a->q_heads % a->kv_heads == 0 && a->head_dim >= 1 && a->ctx >= 1 &&
+           a->ctx <= (1 << 20) && a->max_chunks <= kMaxChunks && a->splits <= kMaxSplits;
+}
+
+extern "C" int64_t q3t_decode_workspace_bytes(const q3t_decode_args *a) {
+    if (!a || !decode_sizes_ok(a)) return -1;
+    return counters_bytes() + partial_floats(a) * 4;
 }
 
 template <typename T, int D, int G, int SQ, bool F, bool M>
 static void launch_decode(const DecodeParams &p, hipStream_t s) {
-    const dim3 grid((uint32_t)p.B * p.Hkv * p.nchunks);
     // streamed instances only for the talker-shaped single-query launches
-    if constexpr (sizeof(T) == 2 && D == 128 && SQ == 1) {
-        if (p.stream) {
-            hipLaunchKernelGGL((decode_attention_kernel<T, D, G, SQ, F, M, true>), grid, dim3(kThreads), 0, s, p);
-            return;
-        }
+    constexpr bool can_stream = sizeof(T) == 2 && D == 128 && SQ == 1;
+    if (p.splits > 0) {
+        const dim3 grid((uint32_t)p.splits * p.Hkv);
+        if (can_stream && p.stream)
+            hipLaunchKernelGGL((decode_balanced_kernel<T, D, G, SQ, F, M, can_stream>), grid, dim3(kThreads), 0, s, p);
+        else
+            hipLaunchKernelGGL((decode_balanced_kernel<T, D, G, SQ, F, M, false>), grid, dim3(kThreads), 0, s, p);
+        return;
     }
-    hipLaunchKernelGGL((decode_attention_kernel<T, D, G, SQ, F, M, false>), grid, dim3(kThreads), 0, s, p);
+    const dim3 grid((uint32_t)p.B * p.Hkv * p.nchunks);
+    if (can_stream && p.stream)
+        hipLaunchKernelGGL((decode_chunks_kernel<T, D, G, SQ, F, M, can_stream>), grid, dim3(kThreads), 0, s, p);
+    else
+        hipLaunchKernelGGL((decode_chunks_kernel<T, D, G, SQ, F, M, false>), grid, dim3(kThreads), 0, s, p);
 }
 
 template <typename T, int D, int G>
 static int dispatch_sq(const DecodeParams &p, int sq, bool fused, hipStream_t s) {
     if (fused) {
         if constexpr (sizeof(T) == 2 && D == 128) {
-            if (p.has_mask) return Q3T_EUNSUPPORTED;
-            if (sq == 1) launch_decode<T, D, G, 1, true, false>(p, s);
-            else if (sq == 2) launch_decode<T, D, G, 2, true, false>(p, s);
-            else return Q3T_EUNSUPPORTED;
+            if (p.has_mask && p.splits <= 0) return Q3T_EUNSUPPORTED;  // masked fused steps run balanced
+            if (sq == 1) {
+                if (p.has_mask) launch_decode<T, D, G, 1, true, true>(p, s);
+                else launch_decode<T, D, G, 1, true, false>(p, s);
+            } else if (sq == 2) {
+                if (p.has_mask) launch_decode<T, D, G, 2, true, true>(p, s);
+                else launch_decode<T, D, G, 2, true, false>(p, s);
+            } else {
+                return Q3T_EUNSUPPORTED;
+            }
             return Q3T_OK;
         } else {
             return Q3T_EUNSUPPORTED;
@@ -666,15 +944,11 @@ static int dispatch_g(const DecodeParams &p, int g, int sq, bool fused, hipStrea
     }
 }
 
-extern "C" int q3t_decode_attention(const q3t_decode_args *a, void *stream) {
-    if (!a) return Q3T_EINVAL;
-    if (a->batch < 0 || a->batch > kMaxBatch || a->query_len < 1 || a->q_heads < 1 ||
-        a->kv_heads < 1 || a->head_dim < 1 || a->ctx < 1 || a->ctx > (1 << 20) ||
-        a->max_chunks > kMaxChunks)
-        return Q3T_EINVAL;
-    if (a->q_heads % a->kv_heads) return Q3T_EINVAL;
+// Host-side validation and parameter set-up shared by every decode entry point; the device
+// workspace (counter region, then the partial states) starts at `ws`.
+static int decode_params(const q3t_decode_args *a, char *ws, DecodeParams &p) {
+    if (!decode_sizes_ok(a)) return Q3T_EINVAL;
     if (a->kv_heads * a->batch > kMaxCounters) return Q3T_EUNSUPPORTED;
-    if (a->batch == 0) return Q3T_OK;
     if (!a->query || !a->keys || !a->values || !a->positions || !a->out) return Q3T_EINVAL;
     if (a->dtype != Q3T_BF16 && a->dtype != Q3T_F32) return Q3T_EUNSUPPORTED;
     if (a->head_dim != 64 && a->head_dim != 128) return Q3T_EUNSUPPORTED;
@@ -701,20 +975,16 @@ extern "C" int q3t_decode_attention(const q3t_decode_args *a, void *stream) {
     // key rows are addressed by 32-bit byte offsets from a request's base
     const int64_t max_st = a->k_stride_t > a->v_stride_t ? a->k_stride_t : a->v_stride_t;
     if (max_st < 0 || a->ctx * max_st * es + a->head_dim * es > INT32_MAX) return Q3T_EUNSUPPORTED;
+    const int64_t splits = balanced_splits(a);
     const int64_t nchunks = chunk_count(a->batch, a->kv_heads, a->ctx, a->max_chunks);
-    if (a->batch * a->kv_heads * nchunks > INT32_MAX) return Q3T_EUNSUPPORTED;
-    const int64_t need = q3t_decode_workspace_bytes(a->batch, a->query_len, a->q_heads, a->kv_heads,
-                                                    a->head_dim, a->ctx, a->max_chunks);
-    if (!a->workspace || a->workspace_bytes < need || !aligned(a->workspace, 16)) return Q3T_EWORKSPACE;
-
-    hipStream_t s = (hipStream_t)stream;
-    char *ws = (char *)a->workspace;
-    DecodeParams p;
+    if (splits > 0 ? splits * a->kv_heads > INT32_MAX : a->batch * a->kv_heads * nchunks > INT32_MAX)
+        return Q3T_EUNSUPPORTED;
     p.B = (int)a->batch;
     p.Hq = (int)a->q_heads;
     p.Hkv = (int)a->kv_heads;
     p.ctx = (int)a->ctx;
     p.nchunks = (int)nchunks;
+    p.splits = (int)splits;
     p.stream = stream_kv(a->batch, a->kv_heads, a->ctx, a->head_dim * es);
     p.scale_log2 = a->scale * kLog2e;
     p.has_mask = a->mask != nullptr;
@@ -747,9 +1017,14 @@ extern "C" int q3t_decode_attention(const q3t_decode_args *a, void *stream) {
         p.qnw = (const char *)a->q_norm_weight;
         p.knw = (const char *)a->k_norm_weight;
     }
+    return Q3T_OK;
+}
 
+static int decode_launch(const q3t_decode_args *a, const DecodeParams &p, void *stream) {
+    hipStream_t s = (hipStream_t)stream;
     const int g = (int)(a->q_heads / a->kv_heads);
     const int sq = (int)a->query_len;
+    const bool fused = a->fused != 0;
     int st;
     if (a->dtype == Q3T_BF16)
         st = a->head_dim == 128 ? dispatch_g<uint16_t, 128>(p, g, sq, fused, s)
@@ -759,4 +1034,31 @@ extern "C" int q3t_decode_attention(const q3t_decode_args *a, void *stream) {
                                 : dispatch_g<float, 64>(p, g, sq, fused, s);
     if (st != Q3T_OK) return st;
     return launch_status();
+}
+
+// Zero the counter region with vector stores (a kernel, not a memset node, so a caller may
+// capture it in a graph).
+__global__ void __launch_bounds__(256) reset_counters_kernel(int4 *counters, int64_t n16) {
+    for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n16; i += (int64_t)gridDim.x * 256)
+        counters[i] = int4{0, 0, 0, 0};
+}
+
+extern "C" int q3t_decode_reset_workspace(void *workspace, int64_t workspace_bytes, void *stream) {
+    if (!workspace || !aligned(workspace, 16) || workspace_bytes < counters_bytes()) return Q3T_EWORKSPACE;
+    const int64_t n16 = counters_bytes() / 16;
+    hipLaunchKernelGGL(reset_counters_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, (int4 *)workspace, n16);
+    return launch_status();
+}
+
+extern "C" int q3t_decode_attention(const q3t_decode_args *a, void *stream) {
+    if (!a) return Q3T_EINVAL;
+    if (!decode_sizes_ok(a)) return Q3T_EINVAL;
+    if (a->batch == 0) return Q3T_OK;
+    DecodeParams p;
+    const int st = decode_params(a, (char *)a->workspace, p);
+    if (st != Q3T_OK) return st;
+    const int64_t need = q3t_decode_workspace_bytes(a);
+    if (!a->workspace || a->workspace_bytes < need || !aligned(a->workspace, 16)) return Q3T_EWORKSPACE;
+    return decode_launch(a, p, stream);
 }

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol(pkg):
 
 def test_status_strings_and_version(pkg):
     lib = pkg.library()
-    assert lib.q3t_abi_version() == 3
+    assert lib.q3t_abi_version() == 4
     assert lib.q3t_status_string(0) == b"success"
     assert lib.q3t_status_string(-1) == b"invalid argument"
     assert lib.q3t_status_string(-3) == b"workspace missing or too small"
@@ -73,15 +73,39 @@ def test_rejected_calls_return_negative_status_without_a_gpu(pkg):
     assert lib.q3t_decode_attention(args, None) == -3   # no workspace
     args.max_chunks = 1025
     assert lib.q3t_decode_attention(args, None) == -1   # more chunks than supported
-    # 256 KiB of counters, then one (G * query_len) x (head_dim + 2) fp32 state per chunk:
-    # ctx 1024 is 16 blocks of 64 keys; chunks are capped by max_chunks, by default at
-    # ceil(512 / (batch * kv_heads)) (1 for 64 requests and 8 KV heads, 8 for 8 requests, all
-    # 16 blocks for 2 requests)
-    assert lib.q3t_decode_workspace_bytes(64, 1, 16, 8, 128, 1024, 0) == 65536 * 4 + 64 * 8 * 1 * 2 * 130 * 4
-    assert lib.q3t_decode_workspace_bytes(8, 1, 16, 8, 128, 1024, 0) == 65536 * 4 + 8 * 8 * 8 * 2 * 130 * 4
-    assert lib.q3t_decode_workspace_bytes(2, 1, 16, 8, 128, 1024, 0) == 65536 * 4 + 2 * 8 * 16 * 2 * 130 * 4
-    assert lib.q3t_decode_workspace_bytes(64, 2, 16, 8, 128, 1024, 4) == 65536 * 4 + 64 * 8 * 4 * 4 * 130 * 4
-    assert lib.q3t_decode_workspace_bytes(64, 1, 16, 8, 128, 1024, 1025) == -1
+    args.max_chunks, args.splits = 0, 32769
+    assert lib.q3t_decode_attention(args, None) == -1   # more splits than supported
+    assert lib.q3t_decode_reset_workspace(None, 1 << 20, None) == -3
+
+
+def _ws(lib, pkg, batch, qlen, ctx, max_chunks=0, splits=0, fused=0, masked=False, dtype=0):
+    a = pkg._lib.DecodeArgs()
+    a.batch, a.query_len, a.q_heads, a.kv_heads, a.head_dim, a.ctx = batch, qlen, 16, 8, 128, ctx
+    a.dtype, a.fused, a.max_chunks, a.splits = dtype, fused, max_chunks, splits
+    a.mask = 16 if masked else None
+    return lib.q3t_decode_workspace_bytes(a)
+
+
+def test_decode_workspace_sizes(pkg):
+    """256 KiB of counters, then one (G * query_len) x (head_dim + 2) fp32 state per part.
+    Chunked grid: ctx 1024 is 16 blocks of 64 keys, chunks capped by max_chunks, by default
+    at ceil(512 / (batch * kv_heads)).  Balanced grid: two state slots per workgroup, by
+    default 256 / kv_heads workgroups per head.  Automatic choice: balanced for contexts of
+    2048 rows or more, or a fused step with a mask; chunked otherwise."""
+    lib = pkg.library()
+    counters = 65536 * 4
+    state = 2 * 130 * 4
+    assert _ws(lib, pkg, 64, 1, 1024) == counters + 64 * 8 * 1 * state              # chunked
+    assert _ws(lib, pkg, 64, 1, 4096) == counters + 8 * 32 * 2 * state              # balanced
+    assert _ws(lib, pkg, 64, 1, 1024, splits=7) == counters + 8 * 7 * 2 * state
+    assert _ws(lib, pkg, 64, 1, 4096, splits=-1) == counters + 64 * 8 * 1 * state    # chunked
+    assert _ws(lib, pkg, 8, 1, 1024) == counters + 8 * 8 * 8 * state
+    assert _ws(lib, pkg, 2, 1, 1024) == counters + 2 * 8 * 16 * state
+    assert _ws(lib, pkg, 64, 2, 1024, max_chunks=4) == counters + 64 * 8 * 4 * 2 * state
+    assert _ws(lib, pkg, 64, 1, 16) == counters + 64 * 8 * 1 * state
+    assert _ws(lib, pkg, 64, 1, 16, fused=1, masked=True) == counters + 8 * 32 * 2 * state
+    assert _ws(lib, pkg, 64, 1, 1024, max_chunks=1025) == -1
+    assert _ws(lib, pkg, 64, 1, 1024, splits=32769) == -1
 
 
 def test_wrappers_reject_cpu_tensors(pkg):

@@ -51,8 +51,8 @@ def test_config1_golden(pkg, device):
     np.testing.assert_allclose(f64(out), g["out"], atol=1e-5, rtol=0)
 
 
-@pytest.mark.parametrize("max_chunks", [0, 4])
-def test_config2_golden_fused_step(pkg, device, max_chunks):
+@pytest.mark.parametrize("splits,max_chunks", [(0, 0), (-1, 4), (300, 0)])
+def test_config2_golden_fused_step(pkg, device, splits, max_chunks):
     g = load("config2_talker64.npz")
     contexts, keys, values, qkv = mg.config2_inputs()
     assert np.array_equal(contexts.numpy(), g["contexts"])
@@ -61,7 +61,7 @@ def test_config2_golden_fused_step(pkg, device, max_chunks):
     q, k, v = mg.split_qkv(dqkv)
     positions = contexts.to(device)
     cos, sin = from_bits(g["cos"], device), from_bits(g["sin"], device)
-    out = pkg.decode_step(q, k, v, dk, dv, positions, cos, sin, max_chunks=max_chunks)
+    out = pkg.decode_step(q, k, v, dk, dv, positions, cos, sin, max_chunks=max_chunks, splits=splits)
     torch.cuda.synchronize()
     assert hashlib.sha256(bits(dk).tobytes()).hexdigest() == str(g["keys_sha256"])
     assert hashlib.sha256(bits(dv).tobytes()).hexdigest() == str(g["values_sha256"])
