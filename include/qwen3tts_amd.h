@@ -199,6 +199,17 @@ int64_t q3t_decode_workspace_bytes(const q3t_decode_args *args);
 
 int q3t_decode_attention(const q3t_decode_args *args, void *stream);
 
+/* q3t_decode_attention without a caller workspace, for callers that cannot allocate device
+   memory (code under graph capture that may not call hipMalloc, tight serving loops,
+   harnesses that forbid allocation).  No counterpart in the reference.  `workspace` and
+   `workspace_bytes` are ignored: the library uses its own fixed 8 MiB device array, one
+   per GPU, held until the process ends (its counters are cleared on the first call on a
+   device, on that call's stream).  A call that would need more than 8 MiB
+   (q3t_decode_workspace_bytes) returns Q3T_EWORKSPACE and launches nothing.  It calls no
+   allocating routine.  Every call on one GPU shares that GPU's array: calls that overlap in
+   time on one GPU (on two streams) race. */
+int q3t_decode_attention_static(const q3t_decode_args *args, void *stream);
+
 /* Re-zero the counter region of a decode workspace on `stream` (a kernel, so it may be
    captured).  Every completed launch leaves the counters zeroed; a launch that failed
    part-way may not, and the next launch that splits a request would then miscount.  No

@@ -98,6 +98,7 @@ SIGNATURES = {
     "q3t_decode_workspace_bytes": (c_i64, [ctypes.POINTER(DecodeArgs)]),
     "q3t_decode_attention": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
     "q3t_decode_reset_workspace": (ctypes.c_int, [c_vp, c_i64, c_vp]),
+    "q3t_decode_attention_static": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
     "q3t_prefill_attention": (ctypes.c_int, [ctypes.POINTER(PrefillArgs), c_vp]),
     "q3t_prefill_rope_write": (ctypes.c_int, [ctypes.POINTER(PrefillRopeWriteArgs), c_vp]),
 }

@@ -82,17 +82,20 @@ def _mask_view(mask, batch, query_len, ctx):
     return mask.expand(batch, query_len, ctx)
 
 
-def _run_decode(args: _lib.DecodeArgs, device: torch.device, what: str) -> None:
+def _run_decode(args: _lib.DecodeArgs, device: torch.device, what: str, no_alloc: bool = False) -> None:
     lib = _lib.library()
     with torch.cuda.device(device):
-        need = lib.q3t_decode_workspace_bytes(args)
-        if need < 0:
-            raise ValueError(f'{what}: invalid sizes')
         stream = _lib.stream_handle(device)
-        ws = workspace(device, need, stream)
-        args.workspace = ws.data_ptr()
-        args.workspace_bytes = ws.numel()
-        status = lib.q3t_decode_attention(args, stream)
+        if no_alloc:
+            status = lib.q3t_decode_attention_static(args, stream)
+        else:
+            need = lib.q3t_decode_workspace_bytes(args)
+            if need < 0:
+                raise ValueError(f'{what}: invalid sizes')
+            ws = workspace(device, need, stream)
+            args.workspace = ws.data_ptr()
+            args.workspace_bytes = ws.numel()
+            status = lib.q3t_decode_attention(args, stream)
     _lib.check(status, what)
 
 
@@ -105,13 +108,15 @@ def _check_out(out, shape, dtype, device, what):
 
 
 def decode_attention(query, keys, values, positions, *, scale=None, mask=None, kv_offsets=None,
-                     out=None, max_chunks=0, splits=0):
+                     out=None, max_chunks=0, splits=0, no_alloc=False):
     """query (B, S, Hq, D) BSND; keys/values (B, Hkv, ctx, D) views of the arena (or, with
     ``kv_offsets``, any base tensor whose request rows start at those element offsets);
     positions (B,) int64: the last query position of each request.  ``splits`` picks the
     grid: > 0 equal shares of each head's keys over that many workgroups, < 0 chunks of
     64-key blocks per request (at most ``max_chunks``, 0: enough for ~512 workgroups),
-    0 automatic.  Returns (B, S, Hq, D)."""
+    0 automatic.  ``no_alloc`` runs the library's allocation-free entry point, which keeps
+    its split states in a fixed per-GPU device array instead of a workspace (calls that
+    overlap in time on one GPU then race).  Returns (B, S, Hq, D)."""
     if query.ndim != 4 or keys.ndim != 4 or values.shape != keys.shape:
         raise ValueError('expected BSND query and BNSD key/value views')
     batch, qlen, q_heads, head_dim = query.shape
@@ -157,13 +162,13 @@ def decode_attention(query, keys, values, positions, *, scale=None, mask=None, k
     a.o_stride_b, a.o_stride_s, a.o_stride_h = out.stride()[:3]
     a.max_chunks = int(max_chunks)
     a.splits = int(splits)
-    _run_decode(a, device, 'decode attention')
+    _run_decode(a, device, 'decode attention', no_alloc)
     return out
 
 
 def decode_step(query, new_key, new_value, key_arena, value_arena, positions, cos, sin, *,
                 scale=None, out=None, max_chunks=0, splits=0, q_norm_weight=None, k_norm_weight=None,
-                norm_eps=1e-6, mask=None):
+                norm_eps=1e-6, mask=None, no_alloc=False):
     """Fused decode step of a layer for one token, or two (the code predictor's first step).
 
     query (B, S, Hq, D), new_key/new_value (B, S, Hkv, D) with S in {1, 2}: un-rotated bf16
@@ -181,7 +186,8 @@ def decode_step(query, new_key, new_value, key_arena, value_arena, positions, co
     ``mask`` (SDPA-style, broadcastable to (B, 1, S, C)) is added to the scores of the keys
     0 ... positions[b], as the reference's operator applies the mask it is given; without it
     request b attends exactly those keys (the ``j <= pos[b]`` mask of SlotGraph.compute).
-    ``splits`` / ``max_chunks`` choose the grid as in ``decode_attention``."""
+    ``splits`` / ``max_chunks`` choose the grid and ``no_alloc`` the allocation-free entry
+    point, as in ``decode_attention``."""
     if (query.ndim != 4 or query.shape[1] not in (1, 2) or new_key.ndim != 4
             or new_key.shape[1] != query.shape[1]):
         raise ValueError('fused decode expects one- or two-token BSND rows')
@@ -246,7 +252,7 @@ def decode_step(query, new_key, new_value, key_arena, value_arena, positions, co
         _lib.require_gpu(weight)
         setattr(a, name, weight.data_ptr())
     a.norm_eps = float(norm_eps)
-    _run_decode(a, device, 'fused decode step')
+    _run_decode(a, device, 'fused decode step', no_alloc)
     return out
 
 

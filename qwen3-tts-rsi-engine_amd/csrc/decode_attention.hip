@@ -29,6 +29,8 @@
 //     output and re-zeroes the pair's counter, so launches can be replayed from a graph.
 #include "q3t_common.hpp"
 
+#include <mutex>
+
 namespace q3t {
 
 constexpr int kMaxBatch = 1024;
@@ -1049,6 +1051,51 @@ extern "C" int q3t_decode_reset_workspace(void *workspace, int64_t workspace_byt
     hipLaunchKernelGGL(reset_counters_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0,
                        (hipStream_t)stream, (int4 *)workspace, n16);
     return launch_status();
+}
+
+// ---- the allocation-free variant --------------------------------------------------------
+// For callers that cannot allocate device memory (code under graph capture that may not call
+// hipMalloc, serving loops, harnesses that forbid it): the workspace is a file-scope device
+// array of a fixed size, one copy per GPU, held until the process ends.  Its device address
+// is looked up once per device (with that device current) and kept; the array's name itself
+// is only a host-side stand-in and is never passed to a kernel.  Every call on one GPU uses
+// the same array: calls that overlap in time on one GPU (two streams) race.
+constexpr int64_t kScratchBytes = 8 << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex scratch_mutex;
+static char *scratch_ptr[kMaxDevices];
+
+// Device address of this device's scratch array (nullptr on failure).  The first call on a
+// device also clears its counter region, on `stream`, before any decode launch that uses it.
+static char *device_scratch(hipStream_t stream) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    if (!scratch_ptr[dev]) {
+        void *ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+        const int64_t n16 = counters_bytes() / 16;
+        hipLaunchKernelGGL(reset_counters_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, stream,
+                           (int4 *)ptr, n16);
+        if (hipGetLastError() != hipSuccess) return nullptr;
+        scratch_ptr[dev] = (char *)ptr;
+    }
+    return scratch_ptr[dev];
+}
+
+extern "C" int q3t_decode_attention_static(const q3t_decode_args *a, void *stream) {
+    if (!a) return Q3T_EINVAL;
+    if (!decode_sizes_ok(a)) return Q3T_EINVAL;
+    if (a->batch == 0) return Q3T_OK;
+    if (q3t_decode_workspace_bytes(a) > kScratchBytes) return Q3T_EWORKSPACE;
+    char *ws = device_scratch((hipStream_t)stream);
+    if (!ws) return (int)hipErrorInvalidDevicePointer;
+    DecodeParams p;
+    const int st = decode_params(a, ws, p);
+    if (st != Q3T_OK) return st;
+    return decode_launch(a, p, stream);
 }
 
 extern "C" int q3t_decode_attention(const q3t_decode_args *a, void *stream) {

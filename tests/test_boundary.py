@@ -76,6 +76,13 @@ def test_rejected_calls_return_negative_status_without_a_gpu(pkg):
     args.max_chunks, args.splits = 0, 32769
     assert lib.q3t_decode_attention(args, None) == -1   # more splits than supported
     assert lib.q3t_decode_reset_workspace(None, 1 << 20, None) == -3
+    # the allocation-free entry point refuses, before touching any device, a call whose split
+    # states would not fit its fixed 8 MiB array (1024 requests x 8 heads x 16 chunks)
+    big = pkg._lib.DecodeArgs()
+    big.batch, big.query_len, big.q_heads, big.kv_heads, big.head_dim, big.ctx = 1024, 1, 16, 8, 128, 1024
+    big.query = big.keys = big.values = big.positions = big.out = 16
+    big.splits, big.max_chunks = -1, 16
+    assert lib.q3t_decode_attention_static(big, None) == -3
 
 
 def _ws(lib, pkg, batch, qlen, ctx, max_chunks=0, splits=0, fused=0, masked=False, dtype=0):
