@@ -186,8 +186,7 @@ typedef struct q3t_decode_args {
     int64_t nk_stride_s, nv_stride_s, cs_stride_s;
     /* grid: > 0 the balanced grid with this many workgroups per KV head (<= 32768; fewer
        run when the keys are few: at least 32 keys per workgroup); < 0 the chunked grid;
-       0 automatic (balanced with 256 workgroups in all for ctx >= 2048 and for fused steps
-       with a mask; chunked otherwise) */
+       0 automatic (balanced with 256 workgroups in all for ctx >= 2048, chunked otherwise) */
     int64_t splits;
 } q3t_decode_args;
 
@@ -222,10 +221,15 @@ int q3t_decode_reset_workspace(void *workspace, int64_t workspace_bytes, void *s
  * query rows (tokens, q_heads, head_dim); key/value rows are read from the slot arena
  * (slot = kv_slots ? kv_slots[b] : b) at positions 0 ... len_b - 1, with strides as in
  * q3t_decode_args.  Query token i of request b attends keys 0 ... i (keys at or past
- * `capacity` do not exist).  max_seqlen bounds len_b; query blocks past it are not computed.
- * bf16 only; head_dim 64 or 128; q_heads / kv_heads in {1, 2, 4}.
- * Replaces: PrefillGraph.compute's padded causal attention (prefill_graph.py:31-50) for
- * the valid rows of each request.
+ * `capacity` do not exist), and with kv_lens only keys below kv_lens[b]: the padded
+ * batch of PrefillGraph.compute, whose mask is key-valid and causal (prefill_graph.py:36-37),
+ * is len_b = the padded length with kv_lens[b] = the prompt's length.  With a mask
+ * (batch, 1, len_b, capacity) the causal rule is off: every key 0 ... capacity - 1 is scored
+ * and the mask is added to the scaled scores, as SDPA adds an attention mask (the drop-in
+ * path for any mask).  A query that sees no key gets a zero row.  max_seqlen bounds len_b;
+ * query blocks past it are not computed.  bf16 only; head_dim 64 or 128;
+ * q_heads / kv_heads in {1, 2, 4}.
+ * Replaces: PrefillGraph.compute's padded causal attention (prefill_graph.py:31-50).
  */
 typedef struct q3t_prefill_args {
     int64_t batch, total_tokens, max_seqlen, q_heads, kv_heads, head_dim;
@@ -246,6 +250,13 @@ typedef struct q3t_prefill_args {
        are already rotated */
     const void *cos, *sin;
     int64_t cs_stride_t;
+    /* optional device (batch,) int32: keys of each request (right-padded batches) */
+    const int32_t *kv_lens;
+    /* optional additive mask, element (b, 0, i, j) at mask + b*mask_stride_b +
+       i*mask_stride_q + j (elements); Q3T_BF16, Q3T_F16 or Q3T_F32 (bool masks are passed as
+       0 / -inf); 16-byte aligned rows */
+    const void *mask;
+    int64_t mask_dtype, mask_stride_b, mask_stride_q;
 } q3t_prefill_args;
 
 int q3t_prefill_attention(const q3t_prefill_args *args, void *stream);

@@ -15,6 +15,8 @@ Modules
   prefill         varlen prefill of packed prompts       (prefill_graph.py)
   scheduler       integer slot state of continuous batching (continuous.py tick/admit)
   slot_graph      SlotGraph: the graph-captured talker decode step (continuous.py SlotGraph)
+  prefill_graph   PrefillGraph / pad_prefill_batch: the graph-captured padded prefill
+                                                         (prefill_graph.py)
 """
 from . import _lib
 from .batching import decode_batch_size
@@ -25,15 +27,17 @@ from .attention import attention, decode_attention, decode_step, prefill_attenti
 from .prefill import prefill_rope_write, prefill_step
 from .packed_attention import PackedAttention, install_packed_attention, restore_modules
 from .scheduler import SlotScheduler, DecodeBatch
-from .slots import SlotArena, SlotCache, PredictorCache, grow_arena
+from .slots import SlotArena, SlotCache, PredictorCache, PrefillCache, grow_arena
 from .slot_graph import SlotGraph
+from .prefill_graph import PrefillGraph, pad_prefill_batch
 
 __all__ = [
     "decode_batch_size", "copy_packed_prefix", "copy_rows", "write", "write_tokens", "rotary",
     "rope_tables", "inverse_frequencies", "attention", "decode_attention", "decode_step",
     "prefill_attention", "prefill_rope_write", "prefill_step", "PackedAttention",
     "install_packed_attention", "restore_modules", "SlotScheduler", "DecodeBatch", "SlotArena",
-    "SlotCache", "PredictorCache", "grow_arena", "SlotGraph", "library",
+    "SlotCache", "PredictorCache", "PrefillCache", "grow_arena", "SlotGraph", "PrefillGraph",
+    "pad_prefill_batch", "library",
 ]
 
 library = _lib.library

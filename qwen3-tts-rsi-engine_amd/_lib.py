@@ -64,6 +64,8 @@ class PrefillArgs(ctypes.Structure):
         ("kv_slots", c_vp), ("out", c_vp), ("o_stride_t", c_i64), ("o_stride_h", c_i64),
         ("capacity", c_i64),
         ("cos", c_vp), ("sin", c_vp), ("cs_stride_t", c_i64),
+        ("kv_lens", c_vp), ("mask", c_vp), ("mask_dtype", c_i64), ("mask_stride_b", c_i64),
+        ("mask_stride_q", c_i64),
     ]
 
 

@@ -240,6 +240,11 @@ def decode_step(query, new_key, new_value, key_arena, value_arena, positions, co
     a.max_chunks = int(max_chunks)
     a.splits = int(splits)
     if mask is not None:
+        # the mask covers keys 0 ... width-1 (SlotGraph's context view, continuous.py:184-192)
+        width = mask.shape[-1]
+        if not 1 <= width <= a.ctx:
+            raise ValueError('the mask is wider than the arena')
+        a.ctx = width
         m = _mask_view(mask.to(device), batch, tokens, a.ctx)
         a.mask = m.data_ptr()
         a.mask_dtype = _lib.DTYPE_CODES[m.dtype]
@@ -254,6 +259,20 @@ def decode_step(query, new_key, new_value, key_arena, value_arena, positions, co
     a.norm_eps = float(norm_eps)
     _run_decode(a, device, 'fused decode step', no_alloc)
     return out
+
+
+_UNIFORM_CU: dict = {}
+
+
+def _uniform_cu(batch, length, device):
+    """Row offsets 0, L, 2L, ... of a (batch, length) padded batch as int32 cu_seqlens, kept
+    per shape so that captured graphs keep using the same tensor."""
+    key = (batch, length, device)
+    cu = _UNIFORM_CU.get(key)
+    if cu is None:
+        cu = _UNIFORM_CU[key] = torch.arange(0, (batch + 1) * length, length, device=device,
+                                             dtype=torch.int32)
+    return cu
 
 
 _LENGTH_POSITIONS: dict = {}
@@ -298,28 +317,35 @@ def attention(module, query, key, value, attention_mask, **kwargs):
         if mask is None and 1 < qlen <= 2 and getattr(module, 'is_causal', True):
             # the reference operator's default for several queries: query i sees keys 0 ... i
             mask = torch.ones(qlen, ctx, device=device, dtype=torch.bool).tril()
-    if mask is not None and qlen > 2:
-        raise ValueError('explicit masks are supported for query lengths up to 2; '
-                         'use prefill_attention for causal prefill')
     if qlen <= 2:
         out = decode_attention(query.transpose(1, 2), key, value, positions, scale=scale, mask=mask)
         return out, None
-    if not getattr(module, 'is_causal', True):
+    if mask is None and not getattr(module, 'is_causal', True):
         raise ValueError('non-causal prefill without a mask is not supported')
-    # causal prefill of equal-length rows: request b's queries sit at positions 0 ... qlen-1
-    cu = torch.arange(0, (batch + 1) * qlen, qlen, device=device, dtype=torch.int32)
+    # several queries per request on the MFMA kernel: without a mask, causal with request b's
+    # queries at positions 0 ... qlen-1; with one (PrefillGraph's key-valid and causal mask,
+    # prefill_graph.py:36-37, or any other) every key is scored and the mask decides
+    cu = _uniform_cu(batch, qlen, device)
     q = query.transpose(1, 2).reshape(batch * qlen, query.shape[1], head_dim)
-    out = prefill_attention(q, key, value, cu, qlen, scale=scale)
+    out = prefill_attention(q, key, value, cu, qlen, scale=scale, mask=mask)
     return out.view(batch, qlen, query.shape[1], head_dim), None
 
 
 def prefill_attention(query, keys, values, cu_seqlens, max_seqlen, *, scale=None, kv_slots=None,
-                      out=None, cos=None, sin=None):
+                      out=None, cos=None, sin=None, kv_lens=None, mask=None):
     """Varlen causal GQA: query (T, Hq, D) packed by cu_seqlens (B+1, int32); keys/values
     (slots, Hkv, capacity, D) arena views holding each request's keys at positions
     0 ... len-1 (slot b, or kv_slots[b]).  Returns (T, Hq, D).  With cos/sin (bf16 (T, D)
     rows of each token's position) the query rows are un-rotated and the kernel applies
-    RoPE as it loads them (bf16-exact, as ``rotary``)."""
+    RoPE as it loads them (bf16-exact, as ``rotary``).
+
+    ``kv_lens`` (int32 (B,), device): request b's queries see only its first kv_lens[b]
+    keys (a right-padded batch: query i sees keys j <= i with j < kv_lens[b], the
+    key-valid and causal mask of PrefillGraph.compute, prefill_graph.py:36-37).
+    ``mask`` (B or 1, 1, len or 1, capacity): an SDPA-style mask (additive bf16 / fp16 /
+    fp32, or bool with True = attend) over every key of the view; the causal rule is then
+    off and the mask alone decides, as with the reference's explicit masks.  A query that
+    sees no key gets a zero row."""
     if query.ndim != 3 or keys.ndim != 4 or values.shape != keys.shape:
         raise ValueError('expected (T, Hq, D) queries and arena key/value views')
     total, q_heads, head_dim = query.shape
@@ -332,10 +358,14 @@ def prefill_attention(query, keys, values, cu_seqlens, max_seqlen, *, scale=None
         raise ValueError('head_dim mismatch or q_heads not a multiple of kv_heads')
     if query.stride(2) != 1 or keys.stride(3) != 1 or values.stride(3) != 1:
         raise ValueError('rows must be unit-stride along head_dim')
-    device = _lib.require_gpu(query, keys, values, cu_seqlens)
     batch = cu_seqlens.numel() - 1
+    if kv_slots is None and keys.shape[0] < batch:
+        raise ValueError('the arena views have fewer slots than requests')
+    device = _lib.require_gpu(query, keys, values, cu_seqlens)
     if out is None:
         out = torch.empty(total, q_heads, head_dim, device=device, dtype=query.dtype)
+    else:
+        _check_out(out, (total, q_heads, head_dim), query.dtype, device, 'prefill attention')
     a = _lib.PrefillArgs()
     a.batch, a.total_tokens, a.max_seqlen = batch, total, int(max_seqlen)
     a.q_heads, a.kv_heads, a.head_dim = q_heads, kv_heads, head_dim
@@ -349,6 +379,7 @@ def prefill_attention(query, keys, values, cu_seqlens, max_seqlen, *, scale=None
     if kv_slots is not None:
         if kv_slots.dtype != torch.int64 or kv_slots.shape != (batch,):
             raise ValueError('kv_slots must be an int64 (B,) tensor')
+        _lib.require_gpu(query, kv_slots)
         a.kv_slots = kv_slots.data_ptr()
     a.out = out.data_ptr()
     a.o_stride_t, a.o_stride_h = out.stride()[:2]
@@ -361,6 +392,42 @@ def prefill_attention(query, keys, values, cu_seqlens, max_seqlen, *, scale=None
             raise ValueError('cos/sin must be bf16 (tokens, head_dim) rows')
         _lib.require_gpu(query, cos, sin)
         a.cos, a.sin, a.cs_stride_t = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
+    if kv_lens is not None:
+        if kv_lens.dtype != torch.int32 or kv_lens.shape != (batch,):
+            raise ValueError('kv_lens must be an int32 (B,) tensor')
+        _lib.require_gpu(query, kv_lens)
+        a.kv_lens = kv_lens.data_ptr()
+    if mask is not None:
+        m = _prefill_mask(mask.to(device), batch, int(max_seqlen), keys.shape[2])
+        a.mask = m.data_ptr()
+        a.mask_dtype = _lib.DTYPE_CODES[m.dtype]
+        a.mask_stride_b, a.mask_stride_q = m.stride(0), m.stride(2)
     status = _lib.library().q3t_prefill_attention(a, _lib.stream_handle(device))
     _lib.check(status, 'prefill attention')
     return out
+
+
+def _prefill_mask(mask, batch, queries, keys):
+    """An SDPA-style (B or 1, 1, Lq or 1, Lk) mask as the kernel reads it: additive bf16 /
+    fp16 / fp32 (bool: True = 0, False = -inf, in bf16), unit-stride keys, 16-byte aligned
+    query rows (broadcast dimensions keep a zero stride)."""
+    if mask.ndim == 2:
+        mask = mask[None, None]
+    elif mask.ndim == 3:
+        mask = mask[:, None]
+    if (mask.ndim != 4 or mask.shape[1] != 1 or mask.shape[0] not in (1, batch)
+            or mask.shape[2] not in (1, queries) or mask.shape[3] != keys):
+        raise ValueError('prefill mask must be (B or 1, 1, Lq or 1, Lk)')
+    if mask.dtype == torch.bool:
+        zero = torch.zeros((), dtype=torch.bfloat16, device=mask.device)
+        mask = torch.where(mask, zero, torch.full_like(zero, float('-inf')))
+    elif mask.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise ValueError('attention mask must be bool, bf16, fp16 or fp32')
+    mask = mask.expand(batch, 1, queries, keys)
+    es = mask.element_size()
+    if (mask.stride(3) != 1 or (mask.stride(2) * es) % 16 or (mask.stride(0) * es) % 16
+            or mask.data_ptr() % 16):
+        mask = mask.contiguous()
+        if (mask.stride(2) * es) % 16:
+            raise ValueError('prefill masks need a key count whose rows are 16-byte multiples')
+    return mask

@@ -859,7 +859,7 @@ static int64_t chunk_count(int64_t batch, int64_t kv_heads, int64_t ctx, int64_t
 static int64_t balanced_splits(const q3t_decode_args *a) {
     if (a->splits < 0) return 0;
     if (a->splits > 0) return a->splits;
-    if (a->ctx < kBalancedMinCtx && !(a->fused && a->mask)) return 0;
+    if (a->ctx < kBalancedMinCtx) return 0;
     return (kBalancedGroups + a->kv_heads - 1) / a->kv_heads;
 }
 
@@ -909,7 +909,6 @@ template <typename T, int D, int G>
 static int dispatch_sq(const DecodeParams &p, int sq, bool fused, hipStream_t s) {
     if (fused) {
         if constexpr (sizeof(T) == 2 && D == 128) {
-            if (p.has_mask && p.splits <= 0) return Q3T_EUNSUPPORTED;  // masked fused steps run balanced
             if (sq == 1) {
                 if (p.has_mask) launch_decode<T, D, G, 1, true, true>(p, s);
                 else launch_decode<T, D, G, 1, true, false>(p, s);

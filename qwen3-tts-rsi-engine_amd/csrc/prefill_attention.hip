@@ -134,6 +134,11 @@ struct PrefillParams {
     int64_t o_st, o_sh;
     const char *cs, *sn;  // optional cos/sin rows per token: the query rows are rotated on load
     int64_t cs_st;
+    const int32_t *kvl;   // optional keys per request (a right-padded batch): query i sees keys
+                          // j <= i with j < kvl[b]
+    const char *mask;     // optional (B, 1, Lq, capacity) additive mask: every key is scored
+    int mdt;              // mask element type (Q3T_BF16, Q3T_F16 or Q3T_F32)
+    int64_t m_sb, m_sq;   // mask strides (elements) of requests and query rows; keys unit-stride
 };
 
 Q3T_DEVICE bf16x8_t as_bf16x8(const U4 &v) { return __builtin_bit_cast(bf16x8_t, v); }
@@ -172,7 +177,36 @@ Q3T_DEVICE void wait_loads() { asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "m
 // Workgroup barrier after the wave's own LDS reads have returned.
 Q3T_DEVICE void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-template <int D, int GH>
+constexpr float kEmptyP = -1.0e30f;  // finite running maximum before any visible key (masked)
+
+// 16 bytes of a mask tile row in LDS -> 4 (2-byte types) or 2 x 2 (fp32: two reads) values in
+// log2 units; positive infinity never occurs in an additive mask, -inf (and finfo.min, which
+// overflows to -inf once scaled) gives a zero weight.
+template <int MB>
+Q3T_DEVICE void mask_values(uint32_t addr, int mdt, float (&mv)[4]) {
+    if constexpr (MB == 2) {
+        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+        const u32x2_t w = *(__attribute__((address_space(3))) const u32x2_t *)(uintptr_t)addr;
+        const uint32_t h[4] = {w.x & 0xffffu, w.x >> 16, w.y & 0xffffu, w.y >> 16};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float v = mdt == Q3T_F16 ? (float)__builtin_bit_cast(_Float16, (uint16_t)h[i])
+                                           : bf16_to_float(h[i]);
+            mv[i] = v * kLog2eP;
+        }
+    } else {
+        const U4 w = lds_read16(addr);
+        const uint32_t f[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mv[i] = __uint_as_float(f[i]) * kLog2eP;
+    }
+}
+
+// MB: bytes per mask element (0: no mask, 2: bf16 / fp16, 4: fp32).  Without a mask the
+// causal rule (and the optional per-request key counts) bounds the key tiles of each query
+// block; with a mask every key tile of the view is scored and the mask alone decides, its
+// tile (64 query rows x 32 keys) staged through the same LDS ring as the keys and values.
+template <int D, int GH, int MB>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GH == 1 ? 4 : 3)))
 prefill_attention_kernel(PrefillParams p) {
     constexpr int NT = 256;                       // threads
@@ -181,8 +215,14 @@ prefill_attention_kernel(PrefillParams p) {
     constexpr int CPR = D / 8;                    // 16-byte chunks per row
     constexpr int ROW = D * 2;                    // bytes per row
     constexpr int KBYTES = kTile * ROW;           // K part of a stage
-    constexpr int SBYTES = 2 * KBYTES;            // stage: K rows, then V rows
+    constexpr int RB = kTile * MB;                // mask bytes per query row of a tile
+    constexpr int MBYTES = kQBlock * RB;          // mask tile of a stage
+    constexpr int SBYTES = 2 * KBYTES + MBYTES;   // stage: K rows, V rows, mask rows
     constexpr int LPT = 2 * kTile * CPR / NT;     // 16-byte loads per thread per tile
+    constexpr int LPR = MB ? RB / 16 : 1;         // lanes per mask row
+    constexpr int RPI = 64 / LPR;                 // mask rows per wave load
+    constexpr int LPTM = MB ? 16 / RPI : 0;       // mask loads per wave per tile (16 rows)
+    constexpr int WAIT = LPT + LPTM;              // loads of one tile per thread
     static_assert(LPT >= 1 && (2 * kTile * CPR) % NT == 0, "a tile is whole loads per thread");
     static_assert(KBYTES % 1024 == 0, "a wave's load never straddles K and V");
     __shared__ __attribute__((aligned(1024))) uint8_t ring[kStages * SBYTES];
@@ -202,12 +242,13 @@ prefill_attention_kernel(PrefillParams p) {
     // in-order dispatch behind them).  Lane i holds request i's row range; each level counts
     // the requests with a block there (ballot) and the item's request is picked by rank
     // (mbcnt), all wave-uniform, with no memory access beyond the row offsets.
-    int b, qb, t0, n;
+    int b, qb, t0, n, kn;
     if (p.B <= 64) {
-        int start = 0, rows = 0;
+        int start = 0, rows = 0, klen = 0;
         if (lane < p.B) {
             start = p.cu[lane];
             rows = (start < 0 || start >= p.T) ? 0 : (int)min((int64_t)(p.cu[lane + 1] - start), p.T - start);
+            klen = p.kvl ? p.kvl[lane] : rows;
         }
         const int blocks = rows > 0 ? (rows + kQBlock - 1) / kQBlock : 0;
         int remaining = rest;
@@ -229,25 +270,30 @@ prefill_attention_kernel(PrefillParams p) {
         if (qb < 0) return;  // past the last block with rows
         t0 = __builtin_amdgcn_readlane(start, b);
         n = __builtin_amdgcn_readlane(rows, b);
+        kn = __builtin_amdgcn_readlane(klen, b);
     } else {
         b = rest % p.B;
         qb = p.nqb - 1 - rest / p.B;  // the longest blocks are dispatched first
         t0 = p.cu[b];
         if (t0 < 0 || t0 >= p.T) return;
         n = (int)min((int64_t)(p.cu[b + 1] - t0), p.T - t0);  // rows past the packed tokens do not exist
+        kn = p.kvl ? p.kvl[b] : n;
     }
     const int q0 = qb * kQBlock;
     if (q0 >= n) return;
-    // keys 0 ... kv_end-1 are visible to this block; the arena holds at most `cap` of them
-    const int kv_end = (int)min((int64_t)min(n, q0 + kQBlock), p.cap);
-    const int ntiles = (kv_end + kTile - 1) / kTile;
+    // keys 0 ... kv_end-1 are visible to this block; the arena holds at most `cap` of them.
+    // Causal: up to the block's last query and the request's key count; masked: every key.
+    const int kv_end = MB ? (int)p.cap : (int)min((int64_t)min(min(n, kn), q0 + kQBlock), p.cap);
+    const int ntiles = kv_end > 0 ? (kv_end + kTile - 1) / kTile : 0;
     const int64_t slot = p.slots ? p.slots[b] : b;
     const int wq0 = q0 + 16 * wave;              // first query of this wave
-    const int wave_end = min(wq0 + 16, kv_end);  // keys [0, wave_end) can be visible to the wave
-    const int mask_from = min(wq0 + 1, kv_end);  // steps reaching past this key need the mask
+    // keys [0, wave_end) can be visible to the wave; steps reaching past mask_from need the
+    // per-key rule (the diagonal or the end of the keys)
+    const int wave_end = MB ? kv_end : min(wq0 + 16, kv_end);
+    const int mask_from = MB ? kv_end : min(wq0 + 1, kv_end);
     const int qpos = wq0 + c;
     const bool qvalid = qpos < n;
-    const int lim = min(qpos, kv_end - 1);       // last key visible to this lane's query
+    const int lim = MB ? kv_end - 1 : min(qpos, kv_end - 1);  // last key visible to this lane's query
 
     // tile loader: load i of a thread fills LDS slot s = i * NT + tid (16 bytes) of a stage:
     // row s / CPR (K rows first, then V rows), physical chunk s % CPR, holding logical chunk
@@ -255,8 +301,12 @@ prefill_attention_kernel(PrefillParams p) {
     const char *kbase = p.k + (slot * p.k_sb + h * p.k_sh) * 2;
     const char *vbase = p.v + (slot * p.v_sb + h * p.v_sh) * 2;
     const uint32_t kst = (uint32_t)(p.k_st * 2), vst = (uint32_t)(p.v_st * 2);
-    const i32x4_t krs = scalar_rsrc(kbase, (uint32_t)((kv_end - 1) * kst + D * 2));
-    const i32x4_t vrs = scalar_rsrc(vbase, (uint32_t)((kv_end - 1) * vst + D * 2));
+    const i32x4_t krs = scalar_rsrc(kbase, kv_end > 0 ? (uint32_t)((kv_end - 1) * kst + D * 2) : 0u);
+    const i32x4_t vrs = scalar_rsrc(vbase, kv_end > 0 ? (uint32_t)((kv_end - 1) * vst + D * 2) : 0u);
+    // mask rows of the request's queries (rows past its queries read zeros)
+    const uint32_t mrow = (uint32_t)(p.m_sq * MB);
+    const i32x4_t mrs = scalar_rsrc(MB ? p.mask + b * p.m_sb * MB : kbase,
+                                    MB ? (uint32_t)((n - 1) * (int64_t)mrow + p.cap * MB) : 0u);
     const uint32_t ring_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)ring;
     uint32_t row_off[LPT];
     int row_of[LPT];
@@ -280,6 +330,17 @@ prefill_attention_kernel(PrefillParams p) {
                                      : 0xfffffff0u;
             load_to_lds16(is_v ? vrs : krs, off,
                           (uint32_t)__builtin_amdgcn_readfirstlane((int)(ring_base + stage * SBYTES + first_slot * 16)));
+        }
+        if constexpr (MB > 0) {
+            // the wave's own 16 query rows of the mask tile: load i covers rows RPI i ... + RPI - 1
+#pragma unroll
+            for (int i = 0; i < LPTM; ++i) {
+                const int r = 16 * wave + i * RPI + lane / LPR;
+                const uint32_t off = q0 + r < n ? (uint32_t)(q0 + r) * mrow + (uint32_t)(kt * RB + (lane % LPR) * 16)
+                                                : 0xfffffff0u;
+                load_to_lds16(mrs, off, (uint32_t)__builtin_amdgcn_readfirstlane(
+                                            (int)(ring_base + stage * SBYTES + 2 * KBYTES + (16 * wave + i * RPI) * RB)));
+            }
         }
     };
 
@@ -359,6 +420,18 @@ prefill_attention_kernel(PrefillParams p) {
         if (kb0 >= wave_end) return;  // past this wave's keys
         const bool masked = kb0 + kTile > mask_from;  // the step reaches past the diagonal or the keys
         const int rel = lim - kb0;
+        float mk[8];
+        if constexpr (MB > 0) {
+            const uint32_t mrow_lds = sbase + 2 * KBYTES + (16 * wave + c) * RB;
+            float lo[4], hi[4];
+            mask_values<MB>(mrow_lds + 4 * g * MB, p.mdt, lo);
+            mask_values<MB>(mrow_lds + (16 + 4 * g) * MB, p.mdt, hi);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                mk[i] = lo[i];
+                mk[4 + i] = hi[i];
+            }
+        }
         bf16x8_t pB[GH];
 #pragma unroll
         for (int j = 0; j < GH; ++j) {
@@ -375,6 +448,10 @@ prefill_attention_kernel(PrefillParams p) {
             }
             __builtin_amdgcn_s_setprio(0);
             float x[8] = {st0[0], st0[1], st0[2], st0[3], st1[0], st1[1], st1[2], st1[3]};
+            if constexpr (MB > 0) {  // scores in log2 units with the mask added
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[e] = __builtin_fmaf(x[e], sl, mk[e]);
+            }
             if (masked) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -387,7 +464,7 @@ prefill_attention_kernel(PrefillParams p) {
             for (int e = 1; e < 8; ++e) mx = __builtin_amdgcn_fmed3f(mx, x[e], __builtin_inff());
             mx = __builtin_amdgcn_fmed3f(mx, xor16(mx), __builtin_inff());
             mx = __builtin_amdgcn_fmed3f(mx, xor32(mx), __builtin_inff());
-            const float mt = mx * sl;
+            const float mt = MB ? fmaxf(mx, kEmptyP) : mx * sl;  // a fully masked step keeps m finite
             if (first) {
                 m[j] = mt;
             } else if (__builtin_amdgcn_ballot_w64(mt > m[j] + kRescaleLog2) != 0) {
@@ -400,7 +477,7 @@ prefill_attention_kernel(PrefillParams p) {
             }
             float pv[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) pv[e] = fexp2(__builtin_fmaf(x[e], sl, -m[j]));
+            for (int e = 0; e < 8; ++e) pv[e] = MB ? fexp2(x[e] - m[j]) : fexp2(__builtin_fmaf(x[e], sl, -m[j]));
             l[j] += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
             const U4 packed = {cvt_pk_bf16(pv[0], pv[1]), cvt_pk_bf16(pv[2], pv[3]),
                                cvt_pk_bf16(pv[4], pv[5]), cvt_pk_bf16(pv[6], pv[7])};
@@ -423,7 +500,7 @@ prefill_attention_kernel(PrefillParams p) {
     // (every wave is done with the stage the next load overwrites), issue the tile
     // kStages - 1 ahead into that stage, then the products
     auto ring_step = [&](int kt, int stage) {
-        if (kt + 1 < ntiles) wait_loads<LPT>();  // the one younger tile stays in flight
+        if (kt + 1 < ntiles) wait_loads<WAIT>();  // the one younger tile stays in flight
         else wait_loads<0>();
         lds_barrier();
         if (kt + kStages - 1 < ntiles) issue(kt + kStages - 1, (stage + kStages - 1) % kStages);
@@ -441,7 +518,7 @@ prefill_attention_kernel(PrefillParams p) {
     for (int j = 0; j < GH; ++j) {
         float lt = l[j] + xor16(l[j]);
         lt += xor32(lt);
-        const float inv = __builtin_amdgcn_rcpf(lt);
+        const float inv = lt > 0.f ? __builtin_amdgcn_rcpf(lt) : 0.f;  // no visible key: zero row
         char *orow = p.out + ((int64_t)(t0 + qpos) * p.o_st + (hq0 + j) * p.o_sh) * 2;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
@@ -499,8 +576,10 @@ extern "C" int q3t_prefill_rope_write(const q3t_prefill_rope_write_args *a, void
 
 template <int D, int GH>
 static void launch_prefill(const PrefillParams &p, hipStream_t s) {
-    hipLaunchKernelGGL((prefill_attention_kernel<D, GH>), dim3((uint32_t)p.B * p.nqb * (p.Hq / GH)),
-                       dim3(256), 0, s, p);
+    const dim3 grid((uint32_t)p.B * p.nqb * (p.Hq / GH));
+    if (!p.mask) hipLaunchKernelGGL((prefill_attention_kernel<D, GH, 0>), grid, dim3(256), 0, s, p);
+    else if (p.mdt == Q3T_F32) hipLaunchKernelGGL((prefill_attention_kernel<D, GH, 4>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((prefill_attention_kernel<D, GH, 2>), grid, dim3(256), 0, s, p);
 }
 
 extern "C" int q3t_prefill_attention(const q3t_prefill_args *a, void *stream) {
@@ -526,6 +605,15 @@ extern "C" int q3t_prefill_attention(const q3t_prefill_args *a, void *stream) {
     // key rows of one (slot, head) are addressed by 32-bit byte offsets
     const int64_t max_st = a->k_stride_t > a->v_stride_t ? a->k_stride_t : a->v_stride_t;
     if (a->capacity * max_st * 2 + a->head_dim * 2 > INT32_MAX) return Q3T_EUNSUPPORTED;
+    if (a->mask) {
+        // rows of 16-byte aligned keys, addressed by 32-bit offsets from a request's base
+        if (a->mask_dtype != Q3T_BF16 && a->mask_dtype != Q3T_F16 && a->mask_dtype != Q3T_F32) return Q3T_EUNSUPPORTED;
+        const int64_t es = a->mask_dtype == Q3T_F32 ? 4 : 2;
+        if (!aligned(a->mask, 16) || a->mask_stride_q < 0 || a->mask_stride_b < 0 || (a->mask_stride_q * es) % 16 ||
+            (a->mask_stride_b * es) % 16)
+            return Q3T_EINVAL;
+        if ((a->max_seqlen - 1) * a->mask_stride_q * es + a->capacity * es > INT32_MAX) return Q3T_EUNSUPPORTED;
+    }
     PrefillParams p;
     p.B = (int)a->batch; p.Hq = (int)a->q_heads; p.Hkv = (int)a->kv_heads;
     p.group = (int)G;
@@ -542,6 +630,10 @@ extern "C" int q3t_prefill_attention(const q3t_prefill_args *a, void *stream) {
     p.T = a->total_tokens;
     p.out = (char *)a->out; p.o_st = a->o_stride_t; p.o_sh = a->o_stride_h;
     p.cs = (const char *)a->cos; p.sn = (const char *)a->sin; p.cs_st = a->cs_stride_t;
+    p.kvl = a->kv_lens;
+    p.mask = (const char *)a->mask;
+    p.mdt = (int)a->mask_dtype;
+    p.m_sb = a->mask_stride_b; p.m_sq = a->mask_stride_q;
     hipStream_t s = (hipStream_t)stream;
     // the query heads of a KV head pair up in one workgroup and share its staged K/V tiles
     if (G % 2 == 0) {

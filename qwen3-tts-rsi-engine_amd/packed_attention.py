@@ -13,8 +13,9 @@ signature compatibility):
 
 * a one-token bf16 step over a ``SlotCache`` is a single ``decode_step`` launch: RoPE of q
   and k, the paired K/V write at the cache positions and ragged GQA attention over keys
-  0 ... position (the ``j <= pos[b]`` mask of SlotGraph.compute, continuous.py:191-192,
-  which the reference adds as 0 / finfo.min);
+  0 ... position, with the layer's mask (SlotGraph.compute's ``j <= pos[b]`` as 0 /
+  finfo.min, continuous.py:191-192) added to the scores as the reference's operator does;
+  rows past a request's position hold stale data and are never read;
 * so is an unmasked one-token step s >= 1 of the code predictor over a ``PredictorCache``:
   it writes position s + 1 and attends positions 0 ... s + 1 (predictor.py:19-24, the
   unmasked steps of UniformPredictor.run, continuous.py:55-62), which is ``decode_step`` with
@@ -37,9 +38,10 @@ from __future__ import annotations
 
 import torch
 
-from .attention import attention, decode_step
+from .attention import attention, decode_step, prefill_attention
+from .prefill import prefill_rope_write
 from .rotary import rotary
-from .slots import PredictorCache, SlotCache
+from .slots import PredictorCache, PrefillCache, SlotCache
 
 _ATTENTION_CLASSES = ('Qwen3TTSTalkerAttention', 'Qwen3TTSAttention')
 
@@ -158,7 +160,11 @@ class PackedAttention(torch.nn.Module):
         return cos, sin
 
     def _fused_target(self, cache, attention_mask, batch, length, query):
-        """(keys, values, positions) of a step the fused launch can take, else None."""
+        """(keys, values, positions, mask) of a step the fused launch can take, else None.
+
+        The mask the layer is given is applied in the launch (the reference's operator applies
+        it, npu_attention.py:16-25), except the predictor's first-step 2x2 causal mask, which
+        is recognised and applied as the causal rule of two queries."""
         reference = self.reference
         if (length not in (1, 2) or reference.training or query.dtype != torch.bfloat16
                 or reference.head_dim != 128):
@@ -170,18 +176,42 @@ class PackedAttention(torch.nn.Module):
                 keys, values = cache.keys[layer], cache.values[layer]
                 if (keys.is_contiguous() and values.is_contiguous() and keys.shape[0] == batch
                         and keys.shape[2] >= 2):
-                    return keys, values, cache.positions_at(batch, 1, query.device)
+                    return keys, values, cache.positions_at(batch, 1, query.device), None
+            return None
+        if attention_mask is not None and not isinstance(attention_mask, torch.Tensor):
             return None
         if isinstance(cache, SlotCache):
             keys, values = cache.arena.keys[layer], cache.arena.values[layer]
             if keys.is_contiguous() and values.is_contiguous():
-                return keys, values, cache.positions
-        elif isinstance(cache, PredictorCache) and cache.step >= 1 and attention_mask is None:
+                return keys, values, cache.positions, attention_mask
+        elif isinstance(cache, PredictorCache) and cache.step >= 1:
             keys, values = cache.keys[layer], cache.values[layer]
             if (keys.is_contiguous() and values.is_contiguous() and keys.shape[0] == batch
                     and cache.step + 1 < keys.shape[2]):
-                return keys, values, cache.positions_at(batch, cache.step + 1, query.device)
+                return keys, values, cache.positions_at(batch, cache.step + 1, query.device), attention_mask
         return None
+
+    def _prefill(self, query, key, value, cos, sin, cache, batch, length):
+        """One layer of a padded prefill batch (PrefillGraph): the module's q/k norms, then the
+        prologue kernel rotating the keys into this layer's planes of the packed cache (the
+        values copied beside them), then causal attention over each row's valid keys with the
+        queries rotated in the kernel.  The layer's mask is not needed: the rows are
+        right-padded prompts and the cache carries their lengths."""
+        reference = self.reference
+        if reference.training:
+            raise ValueError('Native GQA is inference-only')
+        if query.dtype != torch.bfloat16:
+            raise ValueError('padded prefill through PackedAttention is bf16-only')
+        tokens, width = batch * length, reference.head_dim
+        planes = cache.layers[reference.layer_idx]
+        q = reference.q_norm(query).reshape(tokens, -1, width)
+        k = reference.k_norm(key).reshape(tokens, -1, width)
+        v = value.reshape(tokens, -1, width)
+        c, s = cos.reshape(tokens, width), sin.reshape(tokens, width)
+        prefill_rope_write(q, k, v, c, s, cache.cu_seqlens, planes.keys, planes.values, rotate_query=False)
+        out = prefill_attention(q, planes.keys, planes.values, cache.cu_seqlens, length,
+                                scale=reference.scaling, cos=c, sin=s, kv_lens=cache.kv_lens)
+        return reference.o_proj(out.view(batch, length, -1))
 
     def forward(self, hidden_states, position_embeddings, attention_mask, past_key_values=None,
                 cache_position=None, **kwargs):
@@ -194,17 +224,20 @@ class PackedAttention(torch.nn.Module):
         query, key, value = query.reshape(heads), key.reshape(heads), value.reshape(heads)  # BSND
         cos, sin = self._tables(position_embeddings, batch, length)
 
+        if isinstance(past_key_values, PrefillCache):
+            return self._prefill(query, key, value, cos, sin, past_key_values, batch, length), None
+
         fused = self._fused_target(past_key_values, attention_mask, batch, length, query)
         if fused is not None:
-            keys, values, positions = fused
+            keys, values, positions, mask = fused
             if self._norms is not None and self._norms[0].device == query.device:
                 q_weight, k_weight, eps = self._norms
                 output = decode_step(query, key, value, keys, values, positions, cos, sin,
                                      scale=reference.scaling, q_norm_weight=q_weight,
-                                     k_norm_weight=k_weight, norm_eps=eps)
+                                     k_norm_weight=k_weight, norm_eps=eps, mask=mask)
             else:
                 output = decode_step(reference.q_norm(query), reference.k_norm(key), value, keys, values,
-                                     positions, cos, sin, scale=reference.scaling)
+                                     positions, cos, sin, scale=reference.scaling, mask=mask)
             return reference.o_proj(output.reshape(*shape, -1)), None
 
         query = reference.q_norm(query)

@@ -7,6 +7,8 @@ compaction, capacity regrowth) is a HIP kernel of this package.
 """
 from __future__ import annotations
 
+import types
+
 import torch
 from transformers.cache_utils import Cache
 
@@ -168,3 +170,25 @@ class PredictorCache(Cache):
 
     def get_seq_length(self, layer_idx=0):
         return 0 if self.step == 0 else self.step + 1
+
+
+class PrefillCache(Cache):
+    """Per-layer KV of a padded prefill batch, held in one packed
+    ``(2L, batch, kv_heads, length, head_dim)`` buffer (keys first), with the valid length
+    of every row (``kv_lens``, int32, device).  ``layers[i].keys`` / ``.values`` are the
+    ``(batch, kv_heads, length, head_dim)`` planes of layer i, as a ``DynamicCache``'s are."""
+
+    def __init__(self, layers, batch, length, kv_heads, head_dim, device, dtype):
+        super().__init__(layers=[])
+        self.packed = torch.zeros(2 * layers, batch, kv_heads, length, head_dim, device=device, dtype=dtype)
+        self.kv_lens = torch.full((batch,), length, device=device, dtype=torch.int32)
+        self.cu_seqlens = torch.arange(0, (batch + 1) * length, length, device=device, dtype=torch.int32)
+        self.length = length
+        self.layers = [types.SimpleNamespace(keys=self.packed[i], values=self.packed[layers + i])
+                       for i in range(layers)]
+
+    def update(self, keys, values, layer_idx, cache_kwargs=None):
+        raise ValueError('a PrefillCache is written by PackedAttention (install_packed_attention)')
+
+    def get_seq_length(self, layer_idx=0):
+        return self.length

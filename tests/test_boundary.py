@@ -98,7 +98,7 @@ def test_decode_workspace_sizes(pkg):
     Chunked grid: ctx 1024 is 16 blocks of 64 keys, chunks capped by max_chunks, by default
     at ceil(512 / (batch * kv_heads)).  Balanced grid: two state slots per workgroup, by
     default 256 / kv_heads workgroups per head.  Automatic choice: balanced for contexts of
-    2048 rows or more, or a fused step with a mask; chunked otherwise."""
+    2048 rows or more, chunked otherwise."""
     lib = pkg.library()
     counters = 65536 * 4
     state = 2 * 130 * 4
@@ -110,7 +110,7 @@ def test_decode_workspace_sizes(pkg):
     assert _ws(lib, pkg, 2, 1, 1024) == counters + 2 * 8 * 16 * state
     assert _ws(lib, pkg, 64, 2, 1024, max_chunks=4) == counters + 64 * 8 * 4 * 2 * state
     assert _ws(lib, pkg, 64, 1, 16) == counters + 64 * 8 * 1 * state
-    assert _ws(lib, pkg, 64, 1, 16, fused=1, masked=True) == counters + 8 * 32 * 2 * state
+    assert _ws(lib, pkg, 64, 1, 16, fused=1, masked=True) == counters + 64 * 8 * 1 * state
     assert _ws(lib, pkg, 64, 1, 1024, max_chunks=1025) == -1
     assert _ws(lib, pkg, 64, 1, 1024, splits=32769) == -1
 

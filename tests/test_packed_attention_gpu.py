@@ -145,6 +145,51 @@ def test_talker_decode_layer_through_slot_cache(pkg, device, fused_path):
         assert_attention_close(got, expected, max_abs=1e-5, mean_abs=1e-6)
 
 
+@pytest.mark.parametrize("width", [320, 200])
+def test_slot_cache_step_honours_the_layer_mask(pkg, device, width):
+    """The fused launch applies the mask the layer is given, as the reference's operator does
+    (npu_attention.py:16-25): besides j <= pos[b], the mask here also hides every third key
+    and the first key of odd requests, and with width 200 it covers a 200-key context view of
+    the 320-row arena (SlotGraph's context_length, continuous.py:184-192).  The output must
+    follow the oracle under that mask; without honouring it, it would not."""
+    dtype = torch.bfloat16
+    batch, hidden_size, capacity = 16, 256, 320
+    model = _Model(Qwen3TTSTalkerAttention, 1, hidden_size).to(device).eval()
+    pkg.install_packed_attention(model, native_gqa=True, text_only_rope=True, triton_talker_rope=True)
+    module = model.layers[0].self_attn
+    arena = pkg.SlotArena(model, batch, capacity, packed_kv=True)
+    gen = torch.Generator().manual_seed(21)
+    arena.packed.copy_(torch.randn(arena.packed.shape, generator=gen).to(dtype).to(device))
+    contexts = torch.randint(2, width - 1, (batch,), generator=gen)
+    positions = contexts.to(device)
+    cache = pkg.SlotCache(arena, positions, width)
+    hidden = torch.randn(batch, 1, hidden_size, generator=gen).to(dtype).to(device)
+    cos, sin = pkg.rope_tables(positions[:, None], D, dtype=dtype)
+    rope = (cos[None].expand(3, -1, -1, -1), sin[None].expand(3, -1, -1, -1))
+    j = torch.arange(width)[None, :]
+    allowed = (j <= contexts[:, None]) & ((j % 3 != 1) | (j == contexts[:, None]))
+    allowed[1::2, 0] = False
+    mask = torch.where(allowed, 0.0, torch.finfo(dtype).min).to(dtype)[:, None, None, :].to(device)
+    keys_before, values_before = bits(arena.keys[0]).copy(), bits(arena.values[0]).copy()
+    q, k, v = _projected(module, hidden)
+    out, _ = module(hidden, rope, mask, past_key_values=cache, cache_position=positions)
+    torch.cuda.synchronize()
+    cb, sb = bits(cos)[:, :, None, :], bits(sin)[:, :, None, :]
+    q_rot = orope.rope_bf16(bits(q), cb, sb)
+    k_rot = orope.rope_bf16(bits(k), cb, sb)
+    ek, ev = okv.kv_write(keys_before, values_before, k_rot.transpose(0, 2, 1, 3),
+                          bits(v).transpose(0, 2, 1, 3), contexts.numpy())
+    assert np.array_equal(bits(arena.keys[0]), ek) and np.array_equal(bits(arena.values[0]), ev)
+    got = out.detach().float().cpu().numpy().reshape(batch, 1, HQ, D)
+    expected = oatt.decode_attention(obf16.from_bits(q_rot), obf16.from_bits(ek[:, :, :width]),
+                                     obf16.from_bits(ev[:, :, :width]), contexts.numpy(), D ** -0.5,
+                                     mask=allowed.numpy()[:, None, :])
+    assert_attention_close(got, expected)
+    unmasked = oatt.decode_attention(obf16.from_bits(q_rot), obf16.from_bits(ek), obf16.from_bits(ev),
+                                     contexts.numpy(), D ** -0.5)
+    assert np.abs(got - unmasked).max() > 0.1  # the extra masked keys changed the result
+
+
 @pytest.mark.parametrize("kind", ["causal", "none", "full"])
 def test_predictor_first_step_two_queries_with_mask(pkg, device, monkeypatch, kind):
     """Code predictor step 0: two tokens, a PredictorCache writing positions [0, 2).  The 2x2
