@@ -299,44 +299,6 @@ def cpu_baseline(seconds: float, threads: int = 0, dtype=torch.bfloat16):
                        f"cores in the affinity mask) = {layer_s * 1e3:.2f} ms, scaled to a 28-layer step")}
 
 
-def slot_graph_detail(pkg, device, contexts, reps=50, fused_qk_norm=False):
-    """The talker decode step as the reference replays it (SlotGraph.run, continuous.py:217-223):
-    a stand-in talker with the real attention shapes (hidden 2048, 28 layers, 16/8 heads,
-    head_dim 128; input RMSNorm + attention block + residual per layer, no MLP), the drop-in
-    PackedAttention installed, a packed 64-slot arena of capacity 1024 and the seed-0 positions.
-    Per layer: QKV GEMM, q/k RMSNorm, one fused RoPE + K/V write + attention launch, o_proj."""
-    from tests._talker import Talker
-    batch = len(contexts)
-    model = Talker(layers=LAYERS, hidden=2048, q_heads=HQ, kv_heads=HKV, head_dim=D, seed=0).to(device).eval()
-    pkg.install_packed_attention(model, native_gqa=True, text_only_rope=True, triton_talker_rope=True,
-                                 fused_qk_norm=fused_qk_norm)
-    arena = pkg.SlotArena(model, batch, CAPACITY, packed_kv=True)
-    graph = pkg.SlotGraph(arena, batch)
-    graph.capture()
-    gen = torch.Generator().manual_seed(3)
-    inputs = torch.randn(batch, 1, 2048, generator=gen).bfloat16().to(device)
-    positions = contexts.to(device)
-    rotary = positions.view(1, batch, 1).expand(3, batch, 1)
-    for _ in range(3):
-        graph.run(inputs, positions, rotary)
-    torch.cuda.synchronize()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(reps):
-        graph.run(inputs, positions, rotary)
-    stop.record()
-    torch.cuda.synchronize()
-    step_us = start.elapsed_time(stop) * 1e3 / reps
-    graph.close()
-    del graph, arena, model
-    torch.cuda.empty_cache()
-    return {"workload": "SlotGraph.run of a 28-layer talker attention stack (hidden 2048), 64 requests, "
-                        "seed-0 positions, arena capacity 1024",
-            "fused_qk_norm": fused_qk_norm,
-            "us_per_step": step_us, "us_per_layer": step_us / LAYERS,
-            "tokens_per_s": batch / (step_us * 1e-6)}
-
-
 def arena_move_detail(pkg, arena, contexts, reps=20):
     """One compaction move on the talker arena (all 56 planes, capacity 1024): the whole slot
     row, as the reference copies it, against the moved request's prefix [:position + 1]
@@ -475,9 +437,6 @@ def main():
         extra = {"prefill": prefill_detail(pkg, device),
                  "predictor": predictor_detail(pkg, device),
                  "arena_move": arena_move_detail(pkg, arena, contexts),
-                 "talker_attention_step": slot_graph_detail(pkg, device, contexts),
-                 "talker_attention_step_fused_qk_norm": slot_graph_detail(pkg, device, contexts,
-                                                                          fused_qk_norm=True),
                  "reference_probe_shapes": reference_probe_detail(pkg, device)}
     traffic = read_traffic()
     result = {

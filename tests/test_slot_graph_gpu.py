@@ -1,17 +1,27 @@
 """SlotGraph: the talker decode step captured in one HIP graph through PackedAttention.
 
-The graph (continuous.py:170-229 restated on HIP graphs) is checked against the same
-``compute`` run eagerly on a twin arena: every replay's output and the whole arena after it
-must be bit-identical, over several steps with padded rows (positions 0 past the active
-count), with eager work on the stream between replays.  Capture must leave the arena rows at
-position 0 of slots ``[:batch]`` as they were (the reference saves and restores them).  The
-attention numerics themselves are pinned against the oracle in test_packed_attention_gpu.py
-and test_decode_gpu.py.
+The graph (the contract of continuous.py:172-230 on HIP graphs) is checked three ways:
+
+* against the same ``compute`` run eagerly on a twin arena: every replay's output and the
+  whole arena after it bit-identical, over several steps with padded rows (positions 0 past
+  the active count), with eager work on the stream between replays; capture leaves the arena
+  as it was;
+* against an oracle of the whole step on the CPU (the stand-in talker's layers in CPU bf16
+  torch ops, exact RoPE, the scatter write and float64 attention rounded to bf16, i.e. the
+  arithmetic PackedAttention.forward asks for at the same rounding points): the output to
+  max-abs 3e-2 / mean-abs 3e-3 (GEMM accumulation order and fp32 against float64 attention
+  are the only differences), the arena bit-exact against the write of every layer's own
+  projected rows;
+* the mask: not built when every attention layer is wrapped.
 """
 import numpy as np
 import pytest
 import torch
 
+from oracle import attention as oatt
+from oracle import bf16 as obf16
+from oracle import kv as okv
+from oracle import rope as orope
 from tests._talker import Talker
 from tests._util import bits
 
@@ -31,18 +41,15 @@ def _arena(pkg, model, slots, capacity, seed):
     return arena
 
 
-def test_replays_match_eager_compute_and_capture_restores_position_zero(pkg, device):
+def test_replays_match_eager_compute_and_capture_writes_nothing(pkg, device):
     slots, capacity, batch = 16, 192, 8
     model = _model(pkg, device)
     arena = _arena(pkg, model, slots, capacity, 4)
     twin_arena = pkg.SlotArena(model, slots, capacity, packed_kv=True)
     twin_arena.packed.copy_(arena.packed)
-    row0 = bits(arena.packed[:, :batch, :, 0]).copy()
-
     graph = pkg.SlotGraph(arena, batch)
     graph.capture()
     torch.cuda.synchronize()
-    assert np.array_equal(bits(arena.packed[:, :batch, :, 0]), row0)
     assert np.array_equal(bits(arena.packed), bits(twin_arena.packed))
 
     twin = pkg.SlotGraph(twin_arena, batch)
@@ -74,3 +81,97 @@ def test_slot_graph_context_must_fit_the_arena(pkg, device):
         pkg.SlotGraph(arena, 4, context_length=65)
     with pytest.raises(ValueError):
         pkg.SlotGraph(arena, 4, context_length=0)
+
+
+def _cpu_step(talker, arena, inputs, positions, rotary):
+    """The decode step on the CPU: per layer the input norm, the fused QKV projection, the
+    q/k norms (the stand-in's own modules, CPU bf16), exact bf16 RoPE, the paired write at the
+    positions into ``arena`` (bf16 bits, updated in place), float64 attention over keys
+    0 ... position rounded to bf16, o_proj and the residual; then the final norm."""
+    x = inputs.cpu()
+    batch = x.shape[0]
+    cos, sin = talker.rotary_emb(x, rotary.cpu())
+    cb, sb = bits(cos[0])[:, :, None, :], bits(sin[0])[:, :, None, :]
+    layers = len(talker.layers)
+    for index, layer in enumerate(talker.layers):
+        attn = layer.self_attn
+        h = layer.input_layernorm(x)
+        weight = torch.cat([attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight])
+        q, k, v = torch.nn.functional.linear(h, weight).split(
+            [attn.q_proj.out_features, attn.k_proj.out_features, attn.v_proj.out_features], dim=-1)
+        q = attn.q_norm(q.reshape(batch, 1, -1, attn.head_dim))
+        k = attn.k_norm(k.reshape(batch, 1, -1, attn.head_dim))
+        v = v.reshape(batch, 1, -1, attn.head_dim)
+        q_rot, k_rot = orope.rope_bf16(bits(q), cb, sb), orope.rope_bf16(bits(k), cb, sb)
+        okv.kv_write(arena[index], arena[layers + index], k_rot.transpose(0, 2, 1, 3),
+                     bits(v).transpose(0, 2, 1, 3), positions)
+        out = oatt.decode_attention(obf16.from_bits(q_rot), obf16.from_bits(arena[index][:batch]),
+                                    obf16.from_bits(arena[layers + index][:batch]), positions,
+                                    attn.scaling)
+        attended = torch.from_numpy(out).to(torch.bfloat16).reshape(batch, 1, -1)
+        x = x + attn.o_proj(attended)
+    return talker.norm(x)
+
+
+def test_graph_step_matches_the_oracle(pkg, device):
+    slots, capacity, batch, layers, hidden = 16, 256, 12, 3, 512
+    model = _model(pkg, device, layers=layers, hidden=hidden)
+    cpu_talker = Talker(layers=layers, hidden=hidden, seed=3).eval()
+    arena = _arena(pkg, model, slots, capacity, 14)
+    mirror = bits(arena.packed).copy()                        # the oracle's arena
+    twin_arena = pkg.SlotArena(model, slots, capacity, packed_kv=True)
+    graph = pkg.SlotGraph(arena, batch)
+    assert graph._mask(torch.bfloat16) is None                 # every layer is wrapped
+    graph.capture()
+    twin = pkg.SlotGraph(twin_arena, batch)
+    gen = torch.Generator().manual_seed(15)
+    for step, count in enumerate([12, 9]):
+        positions = torch.zeros(batch, dtype=torch.long)
+        positions[:count] = torch.randint(1, capacity, (count,), generator=gen)
+        inputs = torch.randn(batch, 1, hidden, generator=gen).bfloat16()
+        rotary = positions.view(1, batch, 1).expand(3, batch, 1)
+        # the arena each layer must leave: its own projected rows (recorded on an eager twin,
+        # bit-identical to the replay) rotated and written by the oracle
+        twin_arena.packed.copy_(arena.packed)
+        expected_arena = bits(arena.packed).copy()
+        recorded = []
+        hooks = [layer.self_attn.register_forward_hook(
+            lambda module, args, kwargs, out: recorded.append((module, kwargs['hidden_states'])),
+            with_kwargs=True) for layer in model.layers]
+        with torch.inference_mode():
+            twin.inputs.copy_(inputs.to(device))
+            twin.positions.copy_(positions.to(device))
+            twin.rotary.copy_(rotary.to(device))
+            twin.compute()
+        for hook in hooks:
+            hook.remove()
+        cos, sin = model.rotary_emb(inputs.to(device), rotary.to(device))
+        cb, sb = bits(cos[0])[:, :, None, :], bits(sin[0])[:, :, None, :]
+        for index, (module, h) in enumerate(recorded):
+            proj = torch.nn.functional.linear(h, module.weight, module.bias)
+            _, k, v = proj.split(module.sizes, dim=-1)
+            k = module.reference.k_norm(k.reshape(batch, 1, -1, module.reference.head_dim))
+            k_rot = orope.rope_bf16(bits(k), cb, sb)
+            okv.kv_write(expected_arena[index], expected_arena[layers + index], k_rot.transpose(0, 2, 1, 3),
+                         bits(v.reshape(batch, 1, -1, module.reference.head_dim)).transpose(0, 2, 1, 3),
+                         positions.numpy())
+        out = graph.run(inputs.to(device), positions.to(device), rotary.to(device))
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(arena.packed), expected_arena), f"step {step}"
+        expected = _cpu_step(cpu_talker, mirror, inputs, positions.numpy(), rotary)
+        err = (out.float().cpu() - expected.float()).abs()
+        assert err.max().item() <= 3e-2 and err.mean().item() <= 3e-3, (step, err.max().item(), err.mean().item())
+        mirror = bits(arena.packed).copy()                    # next step starts from the device arena
+    graph.close()
+
+
+def test_mask_is_built_only_for_unwrapped_layers(pkg, device):
+    model = Talker(layers=2, hidden=256, seed=3).to(device).eval()
+    arena = pkg.SlotArena(model, 4, 64, packed_kv=True)
+    graph = pkg.SlotGraph(arena, 4, context_length=48)
+    graph.positions.copy_(torch.tensor([0, 5, 47, 10], device=device))
+    mask = graph._mask(torch.bfloat16)
+    assert mask.shape == (4, 1, 1, 48)
+    allowed = torch.arange(48, device=device)[None, :] <= graph.positions[:, None]
+    assert torch.equal(mask[:, 0, 0] == 0, allowed)
+    assert bool((mask[:, 0, 0][~allowed] == torch.finfo(torch.bfloat16).min).all())
