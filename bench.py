@@ -322,6 +322,91 @@ def arena_move_detail(pkg, arena, contexts, reps=20):
     return out
 
 
+def trace_detail(pkg, device, iterations=200, slots=128):
+    """The mixed continuous-batching trace at talker shape: 128 slots, 200 iterations of
+    seeded Poisson arrivals (mean 2 per iteration), prompts U{32..512}, frame limits
+    U{200..2000}, a cancellation of the oldest request with probability 0.2 per iteration,
+    decode bucket step 16 with bucket_kv (continuous.py:425-473, 541-657), over a 28-layer
+    packed arena (capacity 512, growing).  Per iteration: the admissions' prefix loads, the
+    compaction moves and any regrowth (the arena operations), then the 28 fused decode
+    launches at the scheduled positions (zero-position rows of the graph batch included).
+    Reports the decode launches' total time and algorithmic GB/s over the trace, and the
+    arena operations' time.  The scheduler's integer state runs on the host between them."""
+    import numpy as np
+
+    class _Config:
+        num_key_value_heads, head_dim, num_hidden_layers = HKV, D, LAYERS
+
+    class _Talker(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.config = _Config()
+            self.layers = torch.nn.ModuleList([torch.nn.Identity() for _ in range(LAYERS)])
+            self.weight = torch.nn.Parameter(torch.zeros(1, dtype=torch.bfloat16, device=device))
+
+    rng = np.random.default_rng(0)
+    arrivals, cancels, ident = [], [], 0
+    for _ in range(iterations):
+        batch = []
+        for _ in range(int(rng.poisson(2.0))):
+            batch.append((ident, int(rng.integers(32, 513)), int(rng.integers(200, 2001))))
+            ident += 1
+        arrivals.append(batch)
+        cancels.append(float(rng.random()))
+    arena = pkg.SlotArena(_Talker(), slots, 512, packed_kv=True)
+    sched = pkg.SlotScheduler(slots, 512, 16, True, arena=arena)
+    dgen = torch.Generator(device=device).manual_seed(3)
+    qkv = torch.randn(LAYERS, slots, 1, (HQ + 2 * HKV) * D, generator=dgen, device=device, dtype=torch.bfloat16)
+    prefill = torch.randn(2 * LAYERS, 16, HKV, 512, D, generator=dgen, device=device, dtype=torch.bfloat16)
+    out = torch.empty(slots, 1, HQ, D, device=device, dtype=torch.bfloat16)
+    decode_events, arena_events, decode_bytes, launches = [], [], 0, 0
+    queue, active = [], []
+    for it in range(iterations):
+        queue.extend(arrivals[it])
+        cancelled = [active[0]] if active and cancels[it] < 0.2 else []
+        free = slots - (len(active) - len(cancelled))
+        subs, queue = queue[:min(free, prefill.shape[1])], queue[min(free, prefill.shape[1]):]
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        ev[0].record()
+        sched.ops = []
+        sched.cancel(cancelled)
+        sched.admit(subs, prefill)
+        record = sched.decode_batch()
+        ev[1].record()
+        done = []
+        if record is not None:
+            positions = record.positions_tensor(device)
+            cos, sin = pkg.rope_tables(positions, D)
+            b = record.batch
+            ev[2].record()
+            for layer in range(LAYERS):
+                row = qkv[layer, :b]
+                pkg.decode_step(row[..., :HQ * D].view(b, 1, HQ, D),
+                                row[..., HQ * D:(HQ + HKV) * D].view(b, 1, HKV, D),
+                                row[..., (HQ + HKV) * D:].view(b, 1, HKV, D),
+                                sched.arena.keys[layer], sched.arena.values[layer], positions, cos, sin,
+                                out=out[:b])
+            ev[3].record()
+            decode_events.append((ev[2], ev[3]))
+            row_bytes = HKV * D * 2
+            decode_bytes += LAYERS * (sum(record.positions) * row_bytes * 2 + b * row_bytes * 4
+                                      + b * HQ * D * 4 + b * D * 4 + b * 8)
+            launches += LAYERS
+            done = sched.advance()
+        arena_events.append((ev[0], ev[1]))
+        active = [i for i in active if i not in cancelled and i not in done]
+        active.extend(i for i, _, _ in subs if i not in done)
+    torch.cuda.synchronize()
+    decode_us = sum(a.elapsed_time(b) for a, b in decode_events) * 1e3
+    arena_us = sum(a.elapsed_time(b) for a, b in arena_events) * 1e3
+    return {"workload": "128-slot, 200-iteration mixed trace, 28-layer talker arena (8 KV heads, "
+                        "head_dim 128, bf16), eager launches",
+            "final_capacity": sched.capacity, "decode_launches": launches,
+            "decode_us_total": decode_us, "decode_algorithmic_bytes": decode_bytes,
+            "decode_GBs": decode_bytes / (decode_us * 1e-6) / 1e9,
+            "arena_ops_us_total": arena_us}
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -437,6 +522,7 @@ def main():
         extra = {"prefill": prefill_detail(pkg, device),
                  "predictor": predictor_detail(pkg, device),
                  "arena_move": arena_move_detail(pkg, arena, contexts),
+                 "mixed_trace": trace_detail(pkg, device),
                  "reference_probe_shapes": reference_probe_detail(pkg, device)}
     traffic = read_traffic()
     result = {
