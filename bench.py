@@ -407,6 +407,11 @@ def trace_detail(pkg, device, iterations=200, slots=128):
             "arena_ops_us_total": arena_us}
 
 
+KERNELS = {"bundled": "decode_bundled_kernel<G2,fused,streamed>",
+           "balanced": "decode_balanced_kernel<bf16,128,G2,SQ1,fused,streamed>",
+           "chunked": "decode_chunks_kernel<bf16,128,G2,SQ1,fused,streamed>"}
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -415,8 +420,11 @@ def main():
     parser.add_argument("--max-chunks", type=int, default=0,
                         help="chunked grid: 64-key chunks per request and KV head (0 = default)")
     parser.add_argument("--splits", type=int, default=0,
-                        help="decode grid: > 0 balanced with this many workgroups per KV head, "
-                             "< 0 chunked, 0 automatic (balanced for the talker arena)")
+                        help="balanced grid: workgroups per KV head (0: the default); under the "
+                             "automatic grid, > 0 selects balanced and < 0 chunked")
+    parser.add_argument("--grid", choices=["bundled", "balanced", "chunked"], default=None,
+                        help="decode grid by name (default: the library's choice, bundled for "
+                             "this workload)")
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--calibrate-bytes", type=int, default=0,
@@ -461,7 +469,7 @@ def main():
     def step():
         for q, k, v, ak, av, o in views:
             pkg.decode_step(q, k, v, ak, av, positions, cos, sin, out=o, max_chunks=args.max_chunks,
-                            splits=args.splits)
+                            splits=args.splits, grid=args.grid)
 
     step()  # eager: sizes the workspace before capture
     torch.cuda.synchronize()
@@ -491,12 +499,13 @@ def main():
     q0 = views[0][0].contiguous()
     attn_graph = torch.cuda.CUDAGraph()
     pkg.decode_attention(q0, arena[0], arena[LAYERS], positions, max_chunks=args.max_chunks,
-                         splits=args.splits)
+                         splits=args.splits, grid=args.grid)
     torch.cuda.synchronize()
     with torch.cuda.graph(attn_graph):
         for layer in range(LAYERS):
             pkg.decode_attention(q0, arena[layer], arena[LAYERS + layer], positions,
-                                 out=out[layer], max_chunks=args.max_chunks, splits=args.splits)
+                                 out=out[layer], max_chunks=args.max_chunks, splits=args.splits,
+                                 grid=args.grid)
     attn_graph.replay()
     torch.cuda.synchronize()
     reps = max(1, args.steps // 4)
@@ -525,6 +534,8 @@ def main():
                  "mixed_trace": trace_detail(pkg, device),
                  "reference_probe_shapes": reference_probe_detail(pkg, device)}
     traffic = read_traffic()
+    grid_name = pkg.decode_grid_for(BATCH, 1, HQ, HKV, D, CAPACITY, splits=args.splits,
+                                              grid=args.grid)
     result = {
         "metric": "decode-attn tokens/s + achieved HBM GB/s, 64-req ragged talker step, 1 GPU",
         "value": BATCH * args.steps / (gpu_ms / 1e3),
@@ -546,8 +557,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS,
                      "traffic": traffic},
-        "detail": {"kernel": ("decode_chunks_kernel" if args.splits < 0 else "decode_balanced_kernel")
-                             + "<bf16,128,G2,SQ1,fused,streamed>",
+        "detail": {"kernel": KERNELS[grid_name],
+                   "grid": grid_name,
                    "algorithmic_bytes_per_launch": bytes_per_launch,
                    "us_per_layer_launch": launch_us,
                    "us_per_layer_attention_only": attn_us,

@@ -119,14 +119,19 @@ int q3t_rope_tables(const int64_t *positions, int64_t n, const float *inv_freq, 
  * as SDPA does (bool masks: nonzero attends).  Requests with p_b outside [0, ctx) attend
  * nothing and get zero rows.  Query head hq reads KV head hq / (q_heads / kv_heads).
  *
- * Two grids compute the same result.  The balanced grid (`splits` workgroups per KV head)
- * cuts the concatenated keys of all requests of a head into equal shares, one per
- * workgroup, so that ragged lengths keep every workgroup equally busy; it is the default
- * for long contexts (ctx >= 2048).  The chunked grid cuts each request's keys into chunks
- * of 64-key blocks (at most `max_chunks` per request), one workgroup per (request, chunk,
- * KV head); it is the default for shorter contexts (the talker's 1024-row arena, the code
- * predictor's 16-row caches).  A request covered by several workgroups merges their partial
- * softmax states through `workspace`; the last workgroup to finish writes the output.
+ * Three grids compute the same result (to rounding; `grid` picks one, Q3T_GRID_*):
+ *   - bundled: one workgroup per CU, each owning a bundle of whole requests of one KV head
+ *     (requests ranked by length, longest paired with shortest), streamed through LDS and
+ *     scored on bf16 MFMA tiles; no workspace traffic.  bf16, head_dim 128, query_len 1, no
+ *     mask, q_heads / kv_heads <= 4, batch <= 128.  The default for 64..128 requests (times
+ *     kv_heads >= 512) over 1024 <= ctx < 2048 (the talker's 1024-row arena).
+ *   - balanced (`splits` workgroups per KV head): the concatenated keys of all requests of a
+ *     head cut into equal shares, one per workgroup; the default for ctx >= 2048.
+ *   - chunked: each request's keys cut into chunks of 64-key blocks (at most `max_chunks`
+ *     per request), one workgroup per (request, chunk, KV head); the default otherwise (the
+ *     code predictor's 16-row caches, short arenas, few requests).
+ * A request covered by several workgroups (balanced, chunked) merges their partial softmax
+ * states through `workspace`; the last workgroup to finish writes the output.
  *
  * fused != 0 additionally performs, for query_len S in {1, 2} (the step's tokens sit at
  * positions p_b - S + 1 ... p_b):
@@ -184,19 +189,30 @@ typedef struct q3t_decode_args {
     float norm_eps;
     /* fused, S == 2: token strides of new_key, new_value and cos/sin (elements) */
     int64_t nk_stride_s, nv_stride_s, cs_stride_s;
-    /* grid: > 0 the balanced grid with this many workgroups per KV head (<= 32768; fewer
-       run when the keys are few: at least 32 keys per workgroup); < 0 the chunked grid;
-       0 automatic (balanced with 256 workgroups in all for ctx >= 2048, chunked otherwise) */
+    /* balanced grid: workgroups per KV head (<= 32768; fewer run when the keys are few: at
+       least 32 keys per workgroup); 0: 256 workgroups in all.  With grid == Q3T_GRID_AUTO,
+       splits > 0 selects the balanced grid and splits < 0 the chunked grid. */
     int64_t splits;
+    /* Q3T_GRID_AUTO (0), Q3T_GRID_CHUNKED, Q3T_GRID_BALANCED or Q3T_GRID_BUNDLED; a grid the
+       call does not qualify for returns Q3T_EUNSUPPORTED */
+    int64_t grid;
 } q3t_decode_args;
 
+enum { Q3T_GRID_AUTO = 0, Q3T_GRID_CHUNKED = 1, Q3T_GRID_BALANCED = 2, Q3T_GRID_BUNDLED = 3 };
+
 /* Bytes of workspace q3t_decode_attention needs for this call (its sizes, `fused`, `mask`,
-   `max_chunks` and `splits`; pointers are not read); -1 for malformed sizes.  No
+   `max_chunks`, `splits` and `grid`; pointers are not read); -1 for malformed sizes.  No
    counterpart in the reference (its attention operator allocates internally); callers size
    the buffer once, outside graph capture. */
 int64_t q3t_decode_workspace_bytes(const q3t_decode_args *args);
 
 int q3t_decode_attention(const q3t_decode_args *args, void *stream);
+
+/* The grid q3t_decode_attention would run this call on (Q3T_GRID_CHUNKED, _BALANCED or
+   _BUNDLED), from its sizes, `mask`, `splits` and `grid`; Q3T_EUNSUPPORTED when a named grid
+   does not take the call, Q3T_EINVAL for malformed sizes.  No counterpart in the reference
+   (its operator has one implementation). */
+int q3t_decode_grid(const q3t_decode_args *args);
 
 /* q3t_decode_attention without a caller workspace, for callers that cannot allocate device
    memory (code under graph capture that may not call hipMalloc, tight serving loops,

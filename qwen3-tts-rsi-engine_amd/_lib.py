@@ -49,6 +49,7 @@ class DecodeArgs(ctypes.Structure):
         ("q_norm_weight", c_vp), ("k_norm_weight", c_vp), ("norm_eps", ctypes.c_float),
         ("nk_stride_s", c_i64), ("nv_stride_s", c_i64), ("cs_stride_s", c_i64),
         ("splits", c_i64),
+        ("grid", c_i64),
     ]
 
 
@@ -98,6 +99,7 @@ SIGNATURES = {
     "q3t_rope_tables": (ctypes.c_int, [c_vp, c_i64, c_vp, c_i64, ctypes.c_float, c_i64, c_vp,
                                        c_vp, c_vp]),
     "q3t_decode_workspace_bytes": (c_i64, [ctypes.POINTER(DecodeArgs)]),
+    "q3t_decode_grid": (ctypes.c_int, [ctypes.POINTER(DecodeArgs)]),
     "q3t_decode_attention": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
     "q3t_decode_reset_workspace": (ctypes.c_int, [c_vp, c_i64, c_vp]),
     "q3t_decode_attention_static": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
@@ -113,7 +115,7 @@ class KernelError(RuntimeError):
     """A HIP launch failed after host validation passed."""
 
 
-ABI_VERSION = 4  # q3t_abi_version() of the header these structures mirror
+ABI_VERSION = 5  # q3t_abi_version() of the header these structures mirror
 
 
 def library() -> ctypes.CDLL:

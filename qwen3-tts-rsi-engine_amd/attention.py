@@ -107,14 +107,42 @@ def _check_out(out, shape, dtype, device, what):
                          'with unit-stride rows')
 
 
+GRIDS = {None: 0, 'auto': 0, 'chunked': 1, 'balanced': 2, 'bundled': 3}
+
+
+def _grid_code(grid):
+    if grid not in GRIDS:
+        raise ValueError(f"grid must be one of {sorted(k for k in GRIDS if k)} or None")
+    return GRIDS[grid]
+
+
+def decode_grid_for(batch, query_len, q_heads, kv_heads, head_dim, ctx, dtype=torch.bfloat16, *,
+                    masked=False, splits=0, grid=None):
+    """Name of the grid a decode call of these sizes runs on ('bundled', 'balanced' or
+    'chunked'), as the library chooses it (q3t_decode_grid); ValueError when a named grid does
+    not take such a call."""
+    a = _lib.DecodeArgs()
+    a.batch, a.query_len, a.q_heads, a.kv_heads, a.head_dim, a.ctx = batch, query_len, q_heads, kv_heads, head_dim, ctx
+    a.dtype = _lib.DTYPE_CODES[dtype]
+    a.mask = 16 if masked else None
+    a.splits, a.grid = int(splits), _grid_code(grid)
+    code = _lib.library().q3t_decode_grid(a)
+    if code < 0:
+        _lib.check(code, 'decode grid')
+    return {v: k for k, v in GRIDS.items() if k not in (None, 'auto')}[code]
+
+
 def decode_attention(query, keys, values, positions, *, scale=None, mask=None, kv_offsets=None,
-                     out=None, max_chunks=0, splits=0, no_alloc=False):
+                     out=None, max_chunks=0, splits=0, grid=None, no_alloc=False):
     """query (B, S, Hq, D) BSND; keys/values (B, Hkv, ctx, D) views of the arena (or, with
     ``kv_offsets``, any base tensor whose request rows start at those element offsets);
-    positions (B,) int64: the last query position of each request.  ``splits`` picks the
-    grid: > 0 equal shares of each head's keys over that many workgroups, < 0 chunks of
-    64-key blocks per request (at most ``max_chunks``, 0: enough for ~512 workgroups),
-    0 automatic.  ``no_alloc`` runs the library's allocation-free entry point, which keeps
+    positions (B,) int64: the last query position of each request.  ``grid`` picks the
+    kernel grid: 'bundled' (whole requests in length-balanced bundles, one workgroup per CU,
+    bf16 MFMA tiles; one query token, head_dim 128, no mask, up to 128 requests), 'balanced'
+    (equal shares of each head's keys over ``splits`` workgroups per head, 0: 256 in all),
+    'chunked' (chunks of 64-key blocks per request, at most ``max_chunks``, 0: enough for
+    ~512 workgroups) or None for the library's choice, in which ``splits`` > 0 / < 0 still
+    selects balanced / chunked.  ``no_alloc`` runs the library's allocation-free entry point, which keeps
     its split states in a fixed per-GPU device array instead of a workspace (calls that
     overlap in time on one GPU then race).  Returns (B, S, Hq, D)."""
     if query.ndim != 4 or keys.ndim != 4 or values.shape != keys.shape:
@@ -162,13 +190,14 @@ def decode_attention(query, keys, values, positions, *, scale=None, mask=None, k
     a.o_stride_b, a.o_stride_s, a.o_stride_h = out.stride()[:3]
     a.max_chunks = int(max_chunks)
     a.splits = int(splits)
+    a.grid = _grid_code(grid)
     _run_decode(a, device, 'decode attention', no_alloc)
     return out
 
 
 def decode_step(query, new_key, new_value, key_arena, value_arena, positions, cos, sin, *,
-                scale=None, out=None, max_chunks=0, splits=0, q_norm_weight=None, k_norm_weight=None,
-                norm_eps=1e-6, mask=None, no_alloc=False):
+                scale=None, out=None, max_chunks=0, splits=0, grid=None, q_norm_weight=None,
+                k_norm_weight=None, norm_eps=1e-6, mask=None, no_alloc=False):
     """Fused decode step of a layer for one token, or two (the code predictor's first step).
 
     query (B, S, Hq, D), new_key/new_value (B, S, Hkv, D) with S in {1, 2}: un-rotated bf16
@@ -186,8 +215,8 @@ def decode_step(query, new_key, new_value, key_arena, value_arena, positions, co
     ``mask`` (SDPA-style, broadcastable to (B, 1, S, C)) is added to the scores of the keys
     0 ... positions[b], as the reference's operator applies the mask it is given; without it
     request b attends exactly those keys (the ``j <= pos[b]`` mask of SlotGraph.compute).
-    ``splits`` / ``max_chunks`` choose the grid and ``no_alloc`` the allocation-free entry
-    point, as in ``decode_attention``."""
+    ``grid`` / ``splits`` / ``max_chunks`` choose the grid and ``no_alloc`` the
+    allocation-free entry point, as in ``decode_attention``."""
     if (query.ndim != 4 or query.shape[1] not in (1, 2) or new_key.ndim != 4
             or new_key.shape[1] != query.shape[1]):
         raise ValueError('fused decode expects one- or two-token BSND rows')
@@ -239,6 +268,7 @@ def decode_step(query, new_key, new_value, key_arena, value_arena, positions, co
     a.cs_stride_b, a.cs_stride_s = cos3.stride(0), cos3.stride(1)
     a.max_chunks = int(max_chunks)
     a.splits = int(splits)
+    a.grid = _grid_code(grid)
     if mask is not None:
         # the mask covers keys 0 ... width-1 (SlotGraph's context view, continuous.py:184-192)
         width = mask.shape[-1]

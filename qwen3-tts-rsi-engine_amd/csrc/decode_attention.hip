@@ -45,6 +45,7 @@ constexpr int kMinShare = 32;       // balanced grid: fewest keys per workgroup
 struct DecodeParams {
     int B, Hq, Hkv, ctx, nchunks;
     int splits;             // balanced grid: workgroups per KV head (0: chunked grid)
+    int bundles;            // bundled grid: workgroups per KV head (0: another grid)
     float scale_log2;
     int has_mask, mask_dtype;
     const char *q;
@@ -814,6 +815,378 @@ decode_balanced_kernel(DecodeParams p) {
     }
 }
 
+// ---- bundled grid: whole requests in length-balanced bundles, bf16 MFMA tiles -------------
+// For arena-sized single-token launches over many requests (the talker step).  The grid is one
+// workgroup per CU: Hkv x M workgroups, workgroup (m, h) owning bundle m of KV head h.  Each
+// wave ranks the requests by length in registers (the positions, one load round trip; no LDS
+// and no barrier) and takes the requests of ranks m, 2M-1-m, 2M+m, 4M-1-m (snake order): the
+// longest requests are paired with the shortest, so bundles carry about the same number of
+// keys, and each request is attended by one workgroup (no cross-workgroup merge, no workspace).
+//   * K/V rows stream through a ring of kRingStages LDS stages of 64 keys, 16 per wave, loaded
+//     by global-to-LDS buffer loads kRingStages - 1 stages ahead; the waits are explicit, and
+//     the stream runs across request boundaries.  The ring and the per-wave request rows keep
+//     one workgroup per CU.
+//   * each wave scores its 16 keys against the request's G query rows with
+//     v_mfma_f32_16x16x32_bf16 (S^T = K . Q^T: A = 16 key rows from LDS, B = the query rows as
+//     16 columns, G of them live), keeps an online softmax per column in log2 units, and
+//     accumulates O^T += V^T . P^T with v_mfma_f32_16x16x16_bf16 (A = V^T by the transposing
+//     LDS read, B = the bf16 weights straight from the S^T registers).  Rows sit in LDS with
+//     their 16-byte chunks XOR-swizzled (K chunk ch of row r at ch ^ r, V at ch ^ 2r mod 16),
+//     which keeps both reads on distinct banks.
+//   * every wave loads the rows it needs of its requests (query rows and, fused, the cos/sin
+//     rows and new K/V rows) into its own LDS area ahead of the stream, and rotates a request's
+//     query rows (and, in the wave that attends row L-1, the new key) while the request's
+//     first stage is in flight; fused launches place the new key and value in the ring at row
+//     L-1, so the step's key is attended like any other.
+//   * at the end of a request the waves' (max, sum, accumulator) states merge in LDS (two
+//     buffers by request parity); outputs and the new arena rows are stored after the stream,
+//     since a store shares the load counter that the ring waits on.
+constexpr int kBundleGroups = 256;    // workgroups of a launch: one per CU
+constexpr int kBundleMaxBatch = 128;  // requests ranked per launch: two per lane
+constexpr int kBundleMaxSeg = 4;      // requests per bundle
+constexpr int kRingStages = 2;
+constexpr int kStageKeys = 64;
+constexpr int kWaveKeys = kStageKeys / kWaves;  // 16
+constexpr int kRowBytes = 256;                  // bf16 rows of D = 128
+constexpr int kWaveStage = 2 * kWaveKeys * kRowBytes;  // K rows then V rows: 8 KiB
+constexpr int kStageBytes = kWaves * kWaveStage;       // 32 KiB
+constexpr int kStageLoads = 2 * kWaveKeys * kRowBytes / 1024;  // 1 KiB loads per wave and stage: 8
+constexpr float kRescaleLog2 = 8.0f;  // the running maximum moves when exceeded by more than this
+
+template <int G>
+struct BundleLds {
+    char ring[kRingStages][kStageBytes];
+    // per wave and request: rows 0..G-1 query, 4 cos, 5 sin, 6 new K, 7 new V
+    char head[kWaves][kBundleMaxSeg][8][kRowBytes];
+    float acc[2][kWaves][G][128];
+    float ml[2][kWaves][G][2];
+    uint16_t outq[kBundleMaxSeg][G][128];  // bf16 outputs, stored after the stream
+    alignas(16) int keys[kWaves][kBundleMaxBatch];  // each wave's copy of the ranking keys
+};
+
+// The bundle's requests as wave-uniform values (scalar registers): request index, length and
+// row-0 element offsets of its K and V rows, selected by a uniform index without memory (four
+// named slots rather than arrays, which the compiler would place in scratch memory when
+// indexed by a run-time value).
+template <typename X>
+struct Slots4 {
+    X s0, s1, s2, s3;
+    Q3T_DEVICE X get(int k) const { return k == 0 ? s0 : k == 1 ? s1 : k == 2 ? s2 : s3; }
+    Q3T_DEVICE void set(int k, X v) {
+        if (k == 0) s0 = v;
+        else if (k == 1) s1 = v;
+        else if (k == 2) s2 = v;
+        else s3 = v;
+    }
+};
+
+template <int G, bool FUSED, bool STREAM>
+__global__ void __launch_bounds__(kThreads) decode_bundled_kernel(DecodeParams p) {
+    static_assert(G >= 1 && G <= 4, "query rows are the first G of 16 MFMA columns, four LDS rows");
+    __shared__ __attribute__((aligned(16))) BundleLds<G> s;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c = lane & 15;
+    const int h = blockIdx.x % p.Hkv, m = blockIdx.x / p.Hkv, M = p.bundles;
+
+    // weights of the fused norms (chunk c of the row), loaded with the positions and waited for
+    // before any ring load is issued: a wait the compiler placed at their first use would also
+    // wait for the ring's loads, which it does not count
+    U4 qw = {0u, 0u, 0u, 0u}, kw = {0u, 0u, 0u, 0u};
+    if constexpr (FUSED) {
+        if (p.qnw) qw = load16(p.qnw + c * 16);
+        if (p.knw) kw = load16(p.knw + c * 16);
+    }
+    // ranks: key = L * 1024 + (1023 - b) (longest first, ties by index; L = 0 without a valid
+    // position).  Lane holds requests lane and lane + 64; each wave ranks in its own LDS copy
+    // of the keys (no barrier), reading four keys per load.
+    int key[2], len[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int b = lane + 64 * e;
+        int L = 0;
+        if (b < p.B) {
+            const int64_t pb = p.pos[b];
+            L = (pb >= 0 && pb < p.ctx) ? (int)pb + 1 : 0;
+        }
+        len[e] = L;
+        key[e] = b < p.B ? (L << 10) | (1023 - b) : -1;
+        s.keys[wave][b] = key[e];
+    }
+    asm volatile("" :: "v"(qw.x), "v"(kw.x) : "memory");
+    const int nb4 = (p.B + 3) >> 2;
+    int rank[2] = {0, 0};
+    for (int u = 0; u < nb4; ++u) {
+        const i32x4_t k4 = *(const i32x4_t *)&s.keys[wave][4 * u];  // keys past B are -1
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+            rank[e] += (k4.x > key[e]) + (k4.y > key[e]) + (k4.z > key[e]) + (k4.w > key[e]);
+    }
+    // the bundle's requests: ranks m, 2M-1-m, 2M+m, 4M-1-m below B
+    Slots4<int> tb_b = {0, 0, 0, 0}, tb_l = {0, 0, 0, 0};
+    Slots4<int64_t> tb_k = {0, 0, 0, 0}, tb_v = {0, 0, 0, 0};
+    int nseg = 0;
+#pragma unroll
+    for (int i = 0; i < kBundleMaxSeg; ++i) {
+        const int r = (i >> 1) * 2 * M + ((i & 1) ? 2 * M - 1 - m : m);
+        if (r >= p.B) continue;
+        const uint64_t m0 = __builtin_amdgcn_ballot_w64(rank[0] == r && lane < p.B);
+        const uint64_t m1 = __builtin_amdgcn_ballot_w64(rank[1] == r && lane + 64 < p.B);
+        const int b = m0 ? (int)__builtin_ctzll(m0) : 64 + (int)__builtin_ctzll(m1);
+        const int L = m0 ? __builtin_amdgcn_readlane(len[0], b) : __builtin_amdgcn_readlane(len[1], b - 64);
+        const int64_t o = p.offs ? p.offs[b] : 0;
+        tb_b.set(i, b);
+        tb_l.set(i, L);
+        tb_k.set(i, (p.offs ? o : (int64_t)b * p.k_sb) + h * p.k_sh);
+        tb_v.set(i, (p.offs ? o : (int64_t)b * p.v_sb) + h * p.v_sh);
+        nseg = i + 1;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // offsets loaded before any ring load
+
+    auto seg_b = [&](int k) { return tb_b.get(k); };
+    auto seg_l = [&](int k) { return tb_l.get(k); };
+    auto seg_row0 = [&](const char *plane, const Slots4<int64_t> &offsets, int k) {
+        return plane + offsets.get(k) * 2;
+    };
+    auto next_live = [&](int k) {
+        while (k < nseg && seg_l(k) == 0) ++k;
+        return k;
+    };
+    const int first_live = next_live(0);
+    if (first_live >= nseg) {  // nothing to attend (uniform: no load has been issued): zero rows
+        if (wave == 0) {
+            for (int k = 0; k < nseg; ++k) {
+                const int b = seg_b(k);
+                for (int t = lane; t < G * 128; t += 64)
+                    store_out<uint16_t>(p.out + (b * p.o_sb + (h * G + t / 128) * p.o_sh + t % 128) * 2, 0.f);
+            }
+        }
+        return;
+    }
+
+    const int kst = (int)(p.k_st * 2), vst = (int)(p.v_st * 2);
+    const uint32_t kbytes = (uint32_t)((p.ctx - 1) * kst + kRowBytes), vbytes = (uint32_t)((p.ctx - 1) * vst + kRowBytes);
+    const uint32_t lds_ring = (uint32_t)(uintptr_t)&s.ring[0][0];
+    auto head_of = [&](int k) { return (uint32_t)(uintptr_t)&s.head[wave][k][0][0]; };
+
+    // this wave's rows of every request of the bundle, ahead of the ring
+    for (int k = 0; k < nseg; ++k) {
+        const int b = seg_b(k);
+        if (seg_l(k) == 0) continue;
+        const uint32_t hd = (uint32_t)__builtin_amdgcn_readfirstlane((int)head_of(k));
+        const i32x4_t qrs = scalar_rsrc(p.q + (b * p.q_sb + (int64_t)h * G * p.q_sh) * 2,
+                                        (uint32_t)((G - 1) * p.q_sh * 2 + kRowBytes));
+        if (lane < 16 * G) load_to_lds16(qrs, (uint32_t)((lane >> 4) * p.q_sh * 2 + (lane & 15) * 16), hd);
+        if constexpr (FUSED) {
+            const i32x4_t crs = scalar_rsrc(p.cs + b * p.cs_sb * 2, kRowBytes);
+            const i32x4_t srs = scalar_rsrc(p.sn + b * p.cs_sb * 2, kRowBytes);
+            const i32x4_t nkr = scalar_rsrc(p.nk + (b * p.nk_sb + h * p.nk_sh) * 2, kRowBytes);
+            const i32x4_t nvr = scalar_rsrc(p.nv + (b * p.nv_sb + h * p.nv_sh) * 2, kRowBytes);
+            if (lane < 16) {
+                load_to_lds16(crs, lane * 16, hd + 4 * kRowBytes);
+                load_to_lds16(srs, lane * 16, hd + 5 * kRowBytes);
+                load_to_lds16(nkr, lane * 16, hd + 6 * kRowBytes);
+                load_to_lds16(nvr, lane * 16, hd + 7 * kRowBytes);
+            }
+        }
+    }
+
+    // producer: the next stage to load (request index ps, first key pj); past the last request
+    // it loads rows outside the resources (zeros, no memory access), so that every ring step
+    // has the same number of loads in flight behind it
+    int ps = first_live, pj = 0;
+    auto issue = [&](int slot) {
+        const int kq = ps < nseg ? ps : first_live;
+        const int L = ps < nseg ? seg_l(ps) : 0;
+        const int jend = FUSED ? L - 1 : L;  // fused: row L-1 is the step's own key
+        const i32x4_t krs = scalar_rsrc(seg_row0(p.k, tb_k, kq), kbytes);
+        const i32x4_t vrs = scalar_rsrc(seg_row0(p.v, tb_v, kq), vbytes);
+        const uint32_t base = lds_ring + slot * kStageBytes + wave * kWaveStage;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this slot's last reads have returned
+#pragma unroll
+        for (int i = 0; i < kWaveKeys / 4; ++i) {
+            const int r = 4 * i + g, j = pj + wave * kWaveKeys + r;
+            const bool ok = j < jend;
+            const uint32_t ko = ok ? (uint32_t)(j * kst + ((c ^ r) & 15) * 16) : 0xfffffff0u;
+            const uint32_t vo = ok ? (uint32_t)(j * vst + ((c ^ (2 * r)) & 15) * 16) : 0xfffffff0u;
+            const uint32_t kl = (uint32_t)__builtin_amdgcn_readfirstlane((int)(base + i * 1024));
+            const uint32_t vl = (uint32_t)__builtin_amdgcn_readfirstlane((int)(base + kWaveKeys * kRowBytes + i * 1024));
+            if constexpr (STREAM) {
+                load_to_lds16_stream(krs, ko, kl);
+                load_to_lds16_stream(vrs, vo, vl);
+            } else {
+                load_to_lds16(krs, ko, kl);
+                load_to_lds16(vrs, vo, vl);
+            }
+        }
+        if (ps < nseg) {
+            pj += kStageKeys;
+            if (pj >= L) {
+                pj = 0;
+                ps = next_live(ps + 1);
+            }
+        }
+    };
+#pragma unroll
+    for (int st = 0; st < kRingStages - 1; ++st) issue(st);
+
+    // per-lane LDS offsets within a wave's stage: K rows as the A operand of S^T (row c, dims
+    // 32 kk + 8 g ...), V rows for the transposing read (row 4g + c/4, 4 dims)
+    uint32_t ka[4], va[8];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) ka[kk] = c * kRowBytes + (((4 * kk + g) ^ c) & 15) * 16;
+    {
+        const int r = 4 * g + (c >> 2);
+#pragma unroll
+        for (int db = 0; db < 8; ++db)
+            va[db] = kWaveKeys * kRowBytes + r * kRowBytes + (((2 * db + ((c >> 1) & 1)) ^ (2 * r)) & 15) * 16 + 8 * (c & 1);
+    }
+    const float scale = p.scale_log2;
+
+    bf16x8_t qB[4];
+    float mx = kEmpty, l = 0.f;
+    f32x4_t acc[8];
+    int cs = first_live, cj = 0, par = 0;
+    for (int t = 0; cs < nseg; ++t) {
+        issue((t + kRingStages - 1) % kRingStages);
+        const int L = seg_l(cs);
+        const uint32_t hd = head_of(cs);
+        if (cj == 0) {
+            // a new request, while its first stage is in flight: its rows (loaded before every
+            // ring stage) as B operands, columns c >= G zero
+            if (t == 0) wait_loads<kStageLoads * kRingStages>();
+            const U4 zero = {0u, 0u, 0u, 0u};
+            if constexpr (FUSED) {
+                // lane group r: query row r, lane c: chunk c; normalised, rotated, written back
+                const U4 cv = lds_read16(hd + 4 * kRowBytes + c * 16), sv = lds_read16(hd + 5 * kRowBytes + c * 16);
+                U4 x = lds_read16(hd + g * kRowBytes + c * 16);
+                if (p.qnw) x = rms_norm8<16>(x, qw, p.eps, 128);
+                x = rope_half8(x, xor8_u4(x), cv, sv, c < 8);
+                if (g < G) lds_write16(hd + g * kRowBytes + c * 16, x);
+                // the step's key, in the wave that attends row L-1: rotated, kept in row 6
+                if (wave == ((L - 1) % kStageKeys) / kWaveKeys) {
+                    U4 kx = lds_read16(hd + 6 * kRowBytes + c * 16);
+                    if (p.knw) kx = rms_norm8<16>(kx, kw, p.eps, 128);
+                    kx = rope_half8(kx, xor8_u4(kx), cv, sv, c < 8);
+                    if (g == 0) lds_write16(hd + 6 * kRowBytes + c * 16, kx);
+                }
+            }
+            const int cq = c < G ? c : 0;
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const U4 x = lds_read16(hd + cq * kRowBytes + (4 * kk + g) * 16);
+                qB[kk] = as_bf16x8(c < G ? x : zero);
+            }
+            mx = kEmpty;
+            l = 0.f;
+#pragma unroll
+            for (int db = 0; db < 8; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
+        wait_loads<kStageLoads * (kRingStages - 1)>();  // this stage has landed
+        const uint32_t sb = lds_ring + (t % kRingStages) * kStageBytes + wave * kWaveStage;
+        if constexpr (FUSED) {
+            // the step's key and value enter the ring at row L-1 of the request's last stage
+            // (the loads left that row zero)
+            const int r = L - 1 - cj - wave * kWaveKeys;
+            if (r >= 0 && r < kWaveKeys && g == 0) {
+                lds_write16(sb + r * kRowBytes + ((c ^ r) & 15) * 16, lds_read16(hd + 6 * kRowBytes + c * 16));
+                lds_write16(sb + kWaveKeys * kRowBytes + r * kRowBytes + ((c ^ (2 * r)) & 15) * 16,
+                            lds_read16(hd + 7 * kRowBytes + c * 16));
+            }
+        }
+
+        // scores of the wave's 16 keys (rows of S^T) for the 16 columns
+        f32x4_t st = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+            st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(lds_read16(sb + ka[kk])), qB[kk], st, 0, 0, 0);
+        const int j0 = cj + wave * kWaveKeys + 4 * g;
+        float x[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = j0 + i < L ? st[i] * scale : -INFINITY;
+        float mb = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+        mb = fmaxf(mb, xor16(mb));
+        mb = fmaxf(mb, xor32(mb));
+        const bool up = mb > mx + kRescaleLog2;
+        if (__builtin_amdgcn_ballot_w64(up)) {
+            const float mn = up ? mb : mx;
+            const float alpha = fexp2(mx - mn);
+            l *= alpha;
+#pragma unroll
+            for (int db = 0; db < 8; ++db) acc[db] *= alpha;
+            mx = mn;
+        }
+        float pw[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pw[i] = fexp2(x[i] - mx);
+        l += (pw[0] + pw[1]) + (pw[2] + pw[3]);
+        const uint2 pp = {cvt_pk_bf16(pw[0], pw[1]), cvt_pk_bf16(pw[2], pw[3])};
+        const s16x4_t pb = __builtin_bit_cast(s16x4_t, pp);
+#pragma unroll
+        for (int db = 0; db < 8; ++db)
+            acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, lds_read_tr16(sb + va[db])),
+                                                               pb, acc[db], 0, 0, 0);
+
+        cj += kStageKeys;
+        if (cj >= L) {
+            // the request's state: the wave's sums over its lane groups, then the merge of the
+            // four waves in LDS and one output element per thread (kept in LDS)
+            float lt = l + xor16(l);
+            lt += xor32(lt);
+            if (c < G) {
+                if (g == 0) {
+                    s.ml[par][wave][c][0] = mx;
+                    s.ml[par][wave][c][1] = lt;
+                }
+#pragma unroll
+                for (int db = 0; db < 8; ++db)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) s.acc[par][wave][c][16 * db + 4 * g + i] = acc[db][i];
+            }
+            lds_barrier();
+            for (int t2 = tid; t2 < G * 128; t2 += kThreads) {
+                const int cc = t2 / 128, d = t2 % 128;
+                float mm = s.ml[par][0][cc][0];
+#pragma unroll
+                for (int w = 1; w < kWaves; ++w) mm = fmaxf(mm, s.ml[par][w][cc][0]);
+                float sl = 0.f, sa = 0.f;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) {
+                    const float wt = fexp2(s.ml[par][w][cc][0] - mm);
+                    sl += s.ml[par][w][cc][1] * wt;
+                    sa += s.acc[par][w][cc][d] * wt;
+                }
+                s.outq[cs][cc][d] = (uint16_t)float_to_bf16(sa * __builtin_amdgcn_rcpf(sl));
+            }
+            par ^= 1;
+            cs = next_live(cs + 1);
+            cj = 0;
+        }
+    }
+    // stores only now: a store shares the load counter, so one issued during the stream would
+    // hold up the next ring wait until it completed.  Output rows (zeros for requests without a
+    // valid position); fused, the step's key and value rows at L-1 from the wave that rotated
+    // the key (nothing in this launch reads them from the arena).
+    lds_barrier();
+    for (int k = 0; k < nseg; ++k) {
+        const int b = seg_b(k);
+        const int L = seg_l(k);
+        for (int t = tid; t < G * 128; t += kThreads) {
+            const int cc = t / 128, d = t % 128;
+            *reinterpret_cast<uint16_t *>(p.out + (b * p.o_sb + (h * G + cc) * p.o_sh + d) * 2) =
+                L > 0 ? s.outq[k][cc][d] : (uint16_t)0;
+        }
+        if constexpr (FUSED) {
+            if (L > 0 && wave == ((L - 1) % kStageKeys) / kWaveKeys && g == 0) {
+                const uint32_t hd = head_of(k);
+                const auto krs = buffer_rsrc(uniform_ptr(seg_row0(p.k, tb_k, k)), kbytes);
+                const auto vrs = buffer_rsrc(uniform_ptr(seg_row0(p.v, tb_v, k)), vbytes);
+                buffer_store16(krs, (uint32_t)((L - 1) * kst + c * 16), lds_read16(hd + 6 * kRowBytes + c * 16));
+                buffer_store16(vrs, (uint32_t)((L - 1) * vst + c * 16), lds_read16(hd + 7 * kRowBytes + c * 16));
+            }
+        }
+    }
+    wait_loads<0>();  // the trailing ring loads land before the workgroup's LDS is released
+}
+
 // ---------------------------------------------------------------------------------------
 
 // The counter region has one fixed size, so that the counters of every launch sit on bytes
@@ -855,19 +1228,59 @@ static int64_t chunk_count(int64_t batch, int64_t kv_heads, int64_t ctx, int64_t
     return blocks < max_chunks ? blocks : max_chunks;
 }
 
-// The grid a call runs on: > 0 balanced with that many workgroups per KV head, 0 chunked.
+// The grid a call runs on (Q3T_GRID_CHUNKED, _BALANCED or _BUNDLED; -1: a requested grid the
+// call does not qualify for).  The bundled grid needs bf16 rows of 128, one query token, no
+// mask, at most kBundleMaxBatch requests and q_heads / kv_heads <= 4.  Automatic choice,
+// measured (bf16, 16/8 heads, fused and unfused): bundled for 64..128 requests over arenas of
+// 1024 to 2047 rows (64 requests over 1024 rows: 27.6 us against 30.0 chunked and 37.9
+// balanced; 128 requests: 50.4 against 52.1 and 54.8); balanced from 2048 rows (128 requests
+// over 4096 rows: 165 against 169 bundled and 187 chunked); chunked below 1024 rows and for
+// fewer requests (128 requests over 512 rows: 32.0 against 33.9 bundled; 32 over 1024: 21.6
+// against 21.8), where the bundled grid's ranking and start-up are not repaid.
+constexpr int64_t kBundleMinCtx = 1024;
+static bool bundle_ok(const q3t_decode_args *a) {
+    return a->dtype == Q3T_BF16 && a->head_dim == 128 && a->query_len == 1 && !a->mask &&
+           a->batch <= kBundleMaxBatch && a->q_heads / a->kv_heads <= 4;
+}
+static int decode_grid(const q3t_decode_args *a) {
+    switch (a->grid) {
+        case Q3T_GRID_CHUNKED: return Q3T_GRID_CHUNKED;
+        case Q3T_GRID_BALANCED: return Q3T_GRID_BALANCED;
+        case Q3T_GRID_BUNDLED: return bundle_ok(a) ? Q3T_GRID_BUNDLED : -1;
+        default: break;
+    }
+    if (a->splits < 0) return Q3T_GRID_CHUNKED;
+    if (a->splits > 0) return Q3T_GRID_BALANCED;
+    if (bundle_ok(a) && a->batch * a->kv_heads >= 2 * kBundleGroups && a->ctx >= kBundleMinCtx &&
+        a->ctx < kBalancedMinCtx)
+        return Q3T_GRID_BUNDLED;
+    return a->ctx >= kBalancedMinCtx ? Q3T_GRID_BALANCED : Q3T_GRID_CHUNKED;
+}
+
+// Balanced grid: workgroups per KV head.
 static int64_t balanced_splits(const q3t_decode_args *a) {
-    if (a->splits < 0) return 0;
     if (a->splits > 0) return a->splits;
-    if (a->ctx < kBalancedMinCtx) return 0;
     return (kBalancedGroups + a->kv_heads - 1) / a->kv_heads;
+}
+
+// Bundled grid: bundles (workgroups) per KV head, one workgroup per CU in all, and at most
+// kBundleMaxSeg requests per bundle.
+static int64_t bundle_count(const q3t_decode_args *a) {
+    const int64_t m = (kBundleGroups + a->kv_heads - 1) / a->kv_heads;
+    const int64_t least = (a->batch + kBundleMaxSeg - 1) / kBundleMaxSeg;
+    return m < least ? least : m;
 }
 
 static int64_t partial_floats(const q3t_decode_args *a) {
     const int64_t R = (a->q_heads / a->kv_heads) * a->query_len;
-    const int64_t splits = balanced_splits(a);
-    const int64_t units = splits > 0 ? a->kv_heads * splits * 2
-                                     : a->batch * a->kv_heads * chunk_count(a->batch, a->kv_heads, a->ctx, a->max_chunks);
+    int64_t units = 0;
+    switch (decode_grid(a)) {
+        case Q3T_GRID_BALANCED: units = a->kv_heads * balanced_splits(a) * 2; break;
+        case Q3T_GRID_CHUNKED:
+            units = a->batch * a->kv_heads * chunk_count(a->batch, a->kv_heads, a->ctx, a->max_chunks);
+            break;
+        default: break;  // bundled: no partial states
+    }
     return units * R * (a->head_dim + 2);
 }
 
@@ -878,7 +1291,14 @@ using namespace q3t;
 static bool decode_sizes_ok(const q3t_decode_args *a) {
     return a->batch >= 0 && a->batch <= kMaxBatch && a->query_len >= 1 && a->q_heads >= 1 &&
            a->kv_heads >= 1 && a->q_heads % a->kv_heads == 0 && a->head_dim >= 1 && a->ctx >= 1 &&
-           a->ctx <= (1 << 20) && a->max_chunks <= kMaxChunks && a->splits <= kMaxSplits;
+           a->ctx <= (1 << 20) && a->max_chunks <= kMaxChunks && a->splits <= kMaxSplits &&
+           a->grid >= Q3T_GRID_AUTO && a->grid <= Q3T_GRID_BUNDLED;
+}
+
+extern "C" int q3t_decode_grid(const q3t_decode_args *a) {
+    if (!a || !decode_sizes_ok(a)) return Q3T_EINVAL;
+    const int grid = decode_grid(a);
+    return grid < 0 ? Q3T_EUNSUPPORTED : grid;
 }
 
 extern "C" int64_t q3t_decode_workspace_bytes(const q3t_decode_args *a) {
@@ -890,6 +1310,16 @@ template <typename T, int D, int G, int SQ, bool F, bool M>
 static void launch_decode(const DecodeParams &p, hipStream_t s) {
     // streamed instances only for the talker-shaped single-query launches
     constexpr bool can_stream = sizeof(T) == 2 && D == 128 && SQ == 1;
+    if constexpr (sizeof(T) == 2 && D == 128 && SQ == 1 && !M && G <= 4) {
+        if (p.bundles > 0) {
+            const dim3 grid((uint32_t)p.bundles * p.Hkv);
+            if (p.stream)
+                hipLaunchKernelGGL((decode_bundled_kernel<G, F, true>), grid, dim3(kThreads), 0, s, p);
+            else
+                hipLaunchKernelGGL((decode_bundled_kernel<G, F, false>), grid, dim3(kThreads), 0, s, p);
+            return;
+        }
+    }
     if (p.splits > 0) {
         const dim3 grid((uint32_t)p.splits * p.Hkv);
         if (can_stream && p.stream)
@@ -976,7 +1406,9 @@ static int decode_params(const q3t_decode_args *a, char *ws, DecodeParams &p) {
     // key rows are addressed by 32-bit byte offsets from a request's base
     const int64_t max_st = a->k_stride_t > a->v_stride_t ? a->k_stride_t : a->v_stride_t;
     if (max_st < 0 || a->ctx * max_st * es + a->head_dim * es > INT32_MAX) return Q3T_EUNSUPPORTED;
-    const int64_t splits = balanced_splits(a);
+    const int grid = decode_grid(a);
+    if (grid < 0) return Q3T_EUNSUPPORTED;
+    const int64_t splits = grid == Q3T_GRID_BALANCED ? balanced_splits(a) : 0;
     const int64_t nchunks = chunk_count(a->batch, a->kv_heads, a->ctx, a->max_chunks);
     if (splits > 0 ? splits * a->kv_heads > INT32_MAX : a->batch * a->kv_heads * nchunks > INT32_MAX)
         return Q3T_EUNSUPPORTED;
@@ -986,6 +1418,7 @@ static int decode_params(const q3t_decode_args *a, char *ws, DecodeParams &p) {
     p.ctx = (int)a->ctx;
     p.nchunks = (int)nchunks;
     p.splits = (int)splits;
+    p.bundles = grid == Q3T_GRID_BUNDLED ? (int)bundle_count(a) : 0;
     p.stream = stream_kv(a->batch, a->kv_heads, a->ctx, a->head_dim * es);
     p.scale_log2 = a->scale * kLog2e;
     p.has_mask = a->mask != nullptr;

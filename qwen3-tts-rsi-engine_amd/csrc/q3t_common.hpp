@@ -179,4 +179,53 @@ inline int launch_status() {
     return e == hipSuccess ? Q3T_OK : static_cast<int>(e);
 }
 
+// ---- MFMA operands and global-to-LDS loads -------------------------------------------------
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+Q3T_DEVICE bf16x8_t as_bf16x8(const U4 &v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+// 8 bytes of LDS per lane, transposed across each 16-lane group as 16-bit elements.
+Q3T_DEVICE uint2 lds_read_tr16(uint32_t byte_addr) {
+    const s16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4_t *)(uintptr_t)byte_addr);
+    return __builtin_bit_cast(uint2, r);
+}
+Q3T_DEVICE void lds_write16(uint32_t byte_addr, const U4 &v) {
+    *(__attribute__((address_space(3))) i32x4_t *)(uintptr_t)byte_addr = __builtin_bit_cast(i32x4_t, v);
+}
+Q3T_DEVICE U4 lds_read16(uint32_t byte_addr) {
+    const i32x4_t v = *(__attribute__((address_space(3))) const i32x4_t *)(uintptr_t)byte_addr;
+    return __builtin_bit_cast(U4, v);
+}
+
+// A buffer resource in scalar registers (for inline assembly): base, 32-bit range, raw dwords.
+Q3T_DEVICE i32x4_t scalar_rsrc(const void *base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    i32x4_t r;
+    r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    r.y = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu));
+    r.z = __builtin_amdgcn_readfirstlane((int)bytes);
+    r.w = 0x00020000;
+    return r;
+}
+// 16 bytes per lane from global memory straight into LDS at lds_base + 16 * lane (the wave's
+// lanes fill one contiguous 1 KiB run); offsets past the resource's range write zeros.  The
+// load is issued from inline assembly so that the compiler does not insert a wait for it in
+// front of unrelated LDS reads; completion is awaited explicitly with wait_loads.
+Q3T_DEVICE void load_to_lds16(i32x4_t rsrc, uint32_t voffset, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :: "s"(lds_base), "v"(voffset), "s"(rsrc) : "memory", "m0");
+}
+// The same with the non-temporal cache policy, for rows a launch reads once.
+Q3T_DEVICE void load_to_lds16_stream(i32x4_t rsrc, uint32_t voffset, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+                 :: "s"(lds_base), "v"(voffset), "s"(rsrc) : "memory", "m0");
+}
+template <int N>
+Q3T_DEVICE void wait_loads() { asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory"); }
+// Workgroup barrier after the wave's own LDS reads have returned.
+Q3T_DEVICE void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 }  // namespace q3t

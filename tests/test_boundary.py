@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol(pkg):
 
 def test_status_strings_and_version(pkg):
     lib = pkg.library()
-    assert lib.q3t_abi_version() == 4
+    assert lib.q3t_abi_version() == 5
     assert lib.q3t_status_string(0) == b"success"
     assert lib.q3t_status_string(-1) == b"invalid argument"
     assert lib.q3t_status_string(-3) == b"workspace missing or too small"
@@ -75,6 +75,11 @@ def test_rejected_calls_return_negative_status_without_a_gpu(pkg):
     assert lib.q3t_decode_attention(args, None) == -1   # more chunks than supported
     args.max_chunks, args.splits = 0, 32769
     assert lib.q3t_decode_attention(args, None) == -1   # more splits than supported
+    args.splits, args.grid = 0, 4
+    assert lib.q3t_decode_attention(args, None) == -1   # no such grid
+    args.grid, args.query_len = 3, 2
+    assert lib.q3t_decode_attention(args, None) == -2   # two query tokens: not on the bundled grid
+    args.grid, args.query_len = 0, 1
     assert lib.q3t_decode_reset_workspace(None, 1 << 20, None) == -3
     # the allocation-free entry point refuses, before touching any device, a call whose split
     # states would not fit its fixed 8 MiB array (1024 requests x 8 heads x 16 chunks)
@@ -85,10 +90,10 @@ def test_rejected_calls_return_negative_status_without_a_gpu(pkg):
     assert lib.q3t_decode_attention_static(big, None) == -3
 
 
-def _ws(lib, pkg, batch, qlen, ctx, max_chunks=0, splits=0, fused=0, masked=False, dtype=0):
+def _ws(lib, pkg, batch, qlen, ctx, max_chunks=0, splits=0, fused=0, masked=False, dtype=0, grid=0):
     a = pkg._lib.DecodeArgs()
     a.batch, a.query_len, a.q_heads, a.kv_heads, a.head_dim, a.ctx = batch, qlen, 16, 8, 128, ctx
-    a.dtype, a.fused, a.max_chunks, a.splits = dtype, fused, max_chunks, splits
+    a.dtype, a.fused, a.max_chunks, a.splits, a.grid = dtype, fused, max_chunks, splits, grid
     a.mask = 16 if masked else None
     return lib.q3t_decode_workspace_bytes(a)
 
@@ -97,15 +102,28 @@ def test_decode_workspace_sizes(pkg):
     """256 KiB of counters, then one (G * query_len) x (head_dim + 2) fp32 state per part.
     Chunked grid: ctx 1024 is 16 blocks of 64 keys, chunks capped by max_chunks, by default
     at ceil(512 / (batch * kv_heads)).  Balanced grid: two state slots per workgroup, by
-    default 256 / kv_heads workgroups per head.  Automatic choice: balanced for contexts of
-    2048 rows or more, chunked otherwise."""
+    default 256 / kv_heads workgroups per head.  Bundled grid: no partial states.  Automatic
+    choice: bundled for bf16 single-token launches of 64..128 requests (x 8 heads >= 512) over
+    1024..2047 rows, balanced from 2048 rows, chunked otherwise."""
     lib = pkg.library()
     counters = 65536 * 4
     state = 2 * 130 * 4
-    assert _ws(lib, pkg, 64, 1, 1024) == counters + 64 * 8 * 1 * state              # chunked
+    assert _ws(lib, pkg, 64, 1, 1024) == counters                                    # bundled
+    assert _ws(lib, pkg, 128, 1, 2047) == counters                                   # bundled
+    assert _ws(lib, pkg, 129, 1, 1024) == counters + 129 * 8 * 1 * state             # chunked
+    assert _ws(lib, pkg, 63, 1, 1024) == counters + 63 * 8 * 2 * state               # chunked
+    assert _ws(lib, pkg, 64, 1, 1023) == counters + 64 * 8 * 1 * state               # chunked
+    assert _ws(lib, pkg, 64, 1, 1024, dtype=2) == counters + 64 * 8 * 1 * state      # fp32: chunked
+    assert _ws(lib, pkg, 64, 1, 1024, masked=True) == counters + 64 * 8 * 1 * state  # mask: chunked
+    assert _ws(lib, pkg, 64, 1, 1024, grid=1) == counters + 64 * 8 * 1 * state       # named chunked
+    assert _ws(lib, pkg, 64, 1, 1024, grid=2) == counters + 8 * 32 * 2 * state       # named balanced
+    assert _ws(lib, pkg, 8, 1, 64, grid=3) == counters                               # named bundled
+    assert _ws(lib, pkg, 64, 2, 1024, grid=3) == counters  # sized; the launch refuses the grid
+    assert _ws(lib, pkg, 64, 1, 1024, grid=4) == -1       # no such grid
     assert _ws(lib, pkg, 64, 1, 4096) == counters + 8 * 32 * 2 * state              # balanced
     assert _ws(lib, pkg, 64, 1, 1024, splits=7) == counters + 8 * 7 * 2 * state
     assert _ws(lib, pkg, 64, 1, 4096, splits=-1) == counters + 64 * 8 * 1 * state    # chunked
+    assert _ws(lib, pkg, 64, 1, 1024, splits=-1) == counters + 64 * 8 * 1 * state    # chunked
     assert _ws(lib, pkg, 8, 1, 1024) == counters + 8 * 8 * 8 * state
     assert _ws(lib, pkg, 2, 1, 1024) == counters + 2 * 8 * 16 * state
     assert _ws(lib, pkg, 64, 2, 1024, max_chunks=4) == counters + 64 * 8 * 4 * 2 * state
@@ -113,6 +131,29 @@ def test_decode_workspace_sizes(pkg):
     assert _ws(lib, pkg, 64, 1, 16, fused=1, masked=True) == counters + 64 * 8 * 1 * state
     assert _ws(lib, pkg, 64, 1, 1024, max_chunks=1025) == -1
     assert _ws(lib, pkg, 64, 1, 1024, splits=32769) == -1
+
+
+def test_decode_grid_choice(pkg):
+    """The library's grid choice, without a GPU: the talker step (64 requests, 1024-row arena)
+    runs bundled, long arenas balanced, short ones and small batches chunked; splits still
+    selects balanced (> 0) or chunked (< 0) under the automatic choice."""
+    decode_grid_for = pkg.decode_grid_for
+    assert decode_grid_for(64, 1, 16, 8, 128, 1024) == "bundled"
+    assert decode_grid_for(128, 1, 16, 8, 128, 1500) == "bundled"
+    assert decode_grid_for(64, 1, 16, 8, 128, 4096) == "balanced"
+    assert decode_grid_for(64, 1, 16, 8, 128, 16) == "chunked"
+    assert decode_grid_for(32, 1, 16, 8, 128, 1024) == "chunked"
+    assert decode_grid_for(64, 2, 16, 8, 128, 1024) == "chunked"
+    assert decode_grid_for(64, 1, 16, 8, 128, 1024, masked=True) == "chunked"
+    assert decode_grid_for(64, 1, 16, 8, 128, 1024, torch.float32) == "chunked"
+    assert decode_grid_for(64, 1, 16, 8, 128, 1024, splits=-1) == "chunked"
+    assert decode_grid_for(64, 1, 16, 8, 128, 1024, splits=9) == "balanced"
+    assert decode_grid_for(4, 1, 16, 8, 128, 16, grid="bundled") == "bundled"
+    assert decode_grid_for(64, 1, 16, 8, 128, 1024, grid="chunked") == "chunked"
+    with pytest.raises(ValueError):
+        decode_grid_for(64, 2, 16, 8, 128, 1024, grid="bundled")
+    with pytest.raises(ValueError):
+        decode_grid_for(64, 1, 64, 8, 128, 1024, grid="bundled")   # 8 query heads per KV head
 
 
 def test_wrappers_reject_cpu_tensors(pkg):

@@ -89,6 +89,84 @@ def _expected_fused(contexts, k, v, q, kn, vn, cos, sin):
     return ak, av, out
 
 
+@pytest.mark.parametrize("grid", ["bundled", "chunked", "balanced"])
+def test_config2_fused_decode_step_on_each_named_grid(pkg, device, grid):
+    """The headline step on each grid by name (the automatic choice for it is 'bundled')."""
+    contexts, k, v, q, kn, vn = _config2(device, seed=11)
+    positions = contexts.to(device)
+    cos, sin = pkg.rope_tables(positions, D)
+    expected_k, expected_v, expected = _expected_fused(contexts, k, v, q, kn, vn, cos, sin)
+    out = pkg.decode_step(q, kn, vn, k, v, positions, cos, sin, grid=grid)
+    assert np.array_equal(bits(k), expected_k) and np.array_equal(bits(v), expected_v)
+    assert_attention_close(f64(out)[:, 0], expected[:, 0])
+
+
+@pytest.mark.parametrize("group", [1, 2, 4])
+@pytest.mark.parametrize("batch,capacity", [(6, 96), (64, 1024), (128, 640)])
+@pytest.mark.parametrize("fused", [False, True])
+def test_bundled_grid_edges(pkg, device, group, batch, capacity, fused):
+    """The bundled grid (one workgroup per CU, requests ranked by length and bundled longest
+    with shortest, K/V streamed through LDS, bf16 MFMA scores) against the oracle, with the
+    edge lengths: position 0 (only the step's key), the last arena row, lengths on and around
+    the 16- and 64-key boundaries of its tiles, repeated lengths (rank ties), invalid
+    positions (zero rows, nothing written), and bundles left empty (6 requests over 256
+    workgroups)."""
+    gen = torch.Generator().manual_seed(80 + group + batch)
+    kv_heads = HKV if group < 4 else 4
+    q_heads = kv_heads * group
+    contexts = torch.randint(0, capacity, (batch,), generator=gen)
+    edge = torch.tensor([0, capacity - 1, 15, 16, 17, 63, 64, 65, 127, 128, 63, 63, -1, capacity])
+    contexts[:min(batch, len(edge))] = edge[:min(batch, len(edge))]
+    k, v = _arena(batch, capacity, torch.bfloat16, device, 81, kv_heads=kv_heads)
+    q = torch.randn(batch, 1, q_heads, D, generator=gen).bfloat16().to(device)
+    positions = contexts.to(device)
+    valid = (contexts >= 0) & (contexts < capacity)
+    if fused:
+        kn = torch.randn(batch, 1, kv_heads, D, generator=gen).bfloat16().to(device)
+        vn = torch.randn(batch, 1, kv_heads, D, generator=gen).bfloat16().to(device)
+        cos, sin = pkg.rope_tables(positions.clamp(0, capacity - 1), D)
+        before_k, before_v = bits(k).copy(), bits(v).copy()
+        out = pkg.decode_step(q, kn, vn, k, v, positions, cos, sin, grid="bundled")
+        cb, sb = bits(cos)[:, None, None, :], bits(sin)[:, None, None, :]
+        q_rot = obf16.from_bits(orope.rope_bf16(bits(q), cb, sb))
+        k_rot = orope.rope_bf16(bits(kn), cb, sb)
+        ek, ev = before_k.copy(), before_v.copy()
+        for b in np.flatnonzero(valid.numpy()):
+            ek[b, :, contexts[b]] = k_rot[b, 0]
+            ev[b, :, contexts[b]] = bits(vn)[b, 0]
+        assert np.array_equal(bits(k), ek) and np.array_equal(bits(v), ev)
+        keys, values, query = obf16.from_bits(ek), obf16.from_bits(ev), q_rot
+    else:
+        out = pkg.decode_attention(q, k, v, positions, grid="bundled")
+        keys, values, query = f64(k), f64(v), f64(q)
+    got = f64(out)
+    assert not got[~valid.numpy()].any()
+    idx = np.flatnonzero(valid.numpy())
+    expected = oatt.decode_attention(query[idx], keys[idx], values[idx], contexts.numpy()[idx], D ** -0.5)
+    assert_attention_close(got[idx], expected)
+
+
+def test_bundled_grid_is_deterministic_and_refuses_what_it_cannot_run(pkg, device):
+    """Repeated launches are bit-identical; asked for by name, the grid refuses a mask, two
+    query tokens and fp32 rows (the automatic choice runs them on another grid)."""
+    contexts, k, v, q, _, _ = _config2(device, seed=12)
+    positions = contexts.to(device)
+    first = pkg.decode_attention(q, k, v, positions, grid="bundled").clone()
+    for _ in range(10):
+        assert torch.equal(pkg.decode_attention(q, k, v, positions, grid="bundled"), first)
+    expected = oatt.decode_attention(f64(q), f64(k), f64(v), contexts.numpy(), D ** -0.5)
+    assert_attention_close(f64(first), expected)
+    keep = torch.arange(1024, device=device)[None, None, None, :] <= positions[:, None, None, None]
+    with pytest.raises(ValueError, match="unsupported"):
+        pkg.decode_attention(q, k, v, positions, mask=keep, grid="bundled")
+    with pytest.raises(ValueError, match="unsupported"):
+        pkg.decode_attention(q.float(), k.float(), v.float(), positions, grid="bundled")
+    with pytest.raises(ValueError, match="unsupported"):
+        pkg.decode_attention(torch.cat([q, q], 1), k, v, positions, grid="bundled")
+    with pytest.raises(ValueError):
+        pkg.decode_attention(q, k, v, positions, grid="striped")
+
+
 @pytest.mark.parametrize("splits,max_chunks", GRIDS)
 def test_config2_fused_decode_step(pkg, device, splits, max_chunks):
     """The headline step: RoPE + write + ragged GQA over 64 requests, seed 0 (sum c = 32718),
@@ -537,7 +615,8 @@ def test_long_context_multi_block_chunks(pkg, device, splits, max_chunks):
     assert_attention_close(f64(out), expected)
 
 
-def test_kv_offsets_address_any_layout(pkg, device):
+@pytest.mark.parametrize("grid", [None, "bundled"])
+def test_kv_offsets_address_any_layout(pkg, device, grid):
     """kv_offsets place each request's rows at an arbitrary element offset of one buffer
     (a request's keys at offset_b + h * stride_h + j * stride_t)."""
     batch, capacity = 6, 96
@@ -551,12 +630,13 @@ def test_kv_offsets_address_any_layout(pkg, device):
     values = flat_v.view(10, HKV, capacity, D)
     contexts = torch.tensor([95, 10, 40, 0, 63, 77])
     q = torch.randn(batch, 1, HQ, D, generator=gen).bfloat16().to(device)
-    out = pkg.decode_attention(q, keys[:batch], values[:batch], contexts.to(device), kv_offsets=offsets)
+    out = pkg.decode_attention(q, keys[:batch], values[:batch], contexts.to(device), kv_offsets=offsets, grid=grid)
     expected = oatt.decode_attention(f64(q), f64(keys[slots]), f64(values[slots]), contexts.numpy(), D ** -0.5)
     assert_attention_close(f64(out), expected)
 
 
-def test_fused_step_at_position_zero(pkg, device):
+@pytest.mark.parametrize("grid", [None, "bundled"])
+def test_fused_step_at_position_zero(pkg, device, grid):
     """A request at position 0 attends only its own new key: the output is the new value."""
     batch, capacity = 3, 32
     k, v = _arena(batch, capacity, torch.bfloat16, device, 75)
@@ -567,7 +647,7 @@ def test_fused_step_at_position_zero(pkg, device):
     vn = qkv[..., (HQ + HKV) * D:].view(batch, 1, HKV, D)
     positions = torch.zeros(batch, dtype=torch.int64, device=device)
     cos, sin = pkg.rope_tables(positions, D)
-    out = pkg.decode_step(q, kn, vn, k, v, positions, cos, sin)
+    out = pkg.decode_step(q, kn, vn, k, v, positions, cos, sin, grid=grid)
     expected = vn.float().repeat_interleave(HQ // HKV, dim=2)
     assert torch.allclose(out.float(), expected, atol=1e-2, rtol=1e-2)
     assert torch.equal(v[:, :, 0], vn[:, 0])

@@ -31,8 +31,8 @@ def _close_bf16(got_bits, want_bits, frac=0.99):
     assert np.mean(got_bits == want_bits) >= frac, f"bit-equal fraction {np.mean(got_bits == want_bits):.4f}"
 
 
-@pytest.mark.parametrize("eps", [1e-6, 1e-2])
-def test_decode_step_with_qk_norm_matches_oracle(pkg, device, eps):
+@pytest.mark.parametrize("eps,grid", [(1e-6, None), (1e-2, None), (1e-6, "bundled"), (1e-2, "bundled")])
+def test_decode_step_with_qk_norm_matches_oracle(pkg, device, eps, grid):
     gen = torch.Generator().manual_seed(7)
     batch, capacity = 48, 640
     contexts = torch.randint(0, capacity - 1, (batch,), generator=gen)
@@ -48,7 +48,7 @@ def test_decode_step_with_qk_norm_matches_oracle(pkg, device, eps):
     cos, sin = pkg.rope_tables(positions, D)
     k_before, v_before = bits(k).copy(), bits(v).copy()
     out = pkg.decode_step(q, kn, vn, k, v, positions, cos, sin, q_norm_weight=qw, k_norm_weight=kw,
-                          norm_eps=eps)
+                          norm_eps=eps, grid=grid)
     torch.cuda.synchronize()
 
     cb, sb = bits(cos)[:, None, None, :], bits(sin)[:, None, None, :]
