@@ -822,9 +822,9 @@ decode_balanced_kernel(DecodeParams p) {
 // and no barrier) and takes the requests of ranks m, 2M-1-m, 2M+m, 4M-1-m (snake order): the
 // longest requests are paired with the shortest, so bundles carry about the same number of
 // keys, and each request is attended by one workgroup (no cross-workgroup merge, no workspace).
-//   * K/V rows stream through a ring of kRingStages LDS stages of 64 keys, 16 per wave, loaded
-//     by global-to-LDS buffer loads kRingStages - 1 stages ahead; the waits are explicit, and
-//     the stream runs across request boundaries.  The ring and the per-wave request rows keep
+//   * K/V rows stream through two LDS stages of 64 keys, 16 per wave, loaded by global-to-LDS
+//     buffer loads one stage ahead of the one being scored; the waits are explicit, and the
+//     stream runs across request boundaries.  The ring and the per-wave request rows keep
 //     one workgroup per CU.
 //   * each wave scores its 16 keys against the request's G query rows with
 //     v_mfma_f32_16x16x32_bf16 (S^T = K . Q^T: A = 16 key rows from LDS, B = the query rows as
@@ -844,6 +844,9 @@ decode_balanced_kernel(DecodeParams p) {
 constexpr int kBundleGroups = 256;    // workgroups of a launch: one per CU
 constexpr int kBundleMaxBatch = 128;  // requests ranked per launch: two per lane
 constexpr int kBundleMaxSeg = 4;      // requests per bundle
+// K/V stages: the one being scored and the next one in flight.  Measured on the talker step:
+// two stages in flight (three LDS stages) 27.6 us against 26.5 us with one; two only over a
+// workgroup's last 4 or 8 stages, no gain either.
 constexpr int kRingStages = 2;
 constexpr int kStageKeys = 64;
 constexpr int kWaveKeys = kStageKeys / kWaves;  // 16
@@ -983,19 +986,21 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(DecodeParams p
             if (lane < 16) {
                 load_to_lds16(crs, lane * 16, hd + 4 * kRowBytes);
                 load_to_lds16(srs, lane * 16, hd + 5 * kRowBytes);
+            }
+            // the step's key and value only in the wave that attends row L-1
+            if (lane < 16 && wave == ((seg_l(k) - 1) % kStageKeys) / kWaveKeys) {
                 load_to_lds16(nkr, lane * 16, hd + 6 * kRowBytes);
                 load_to_lds16(nvr, lane * 16, hd + 7 * kRowBytes);
             }
         }
     }
 
-    // producer: the next stage to load (request index ps, first key pj); past the last request
-    // it loads rows outside the resources (zeros, no memory access), so that every ring step
-    // has the same number of loads in flight behind it
+    // producer: the next stage to load (request index ps, first key pj); rows at or past the
+    // request's keys get offsets outside the resource (zeros, no memory access)
     int ps = first_live, pj = 0;
     auto issue = [&](int slot) {
-        const int kq = ps < nseg ? ps : first_live;
-        const int L = ps < nseg ? seg_l(ps) : 0;
+        const int kq = ps;
+        const int L = seg_l(ps);
         const int jend = FUSED ? L - 1 : L;  // fused: row L-1 is the step's own key
         const i32x4_t krs = scalar_rsrc(seg_row0(p.k, tb_k, kq), kbytes);
         const i32x4_t vrs = scalar_rsrc(seg_row0(p.v, tb_v, kq), vbytes);
@@ -1017,16 +1022,20 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(DecodeParams p
                 load_to_lds16(vrs, vo, vl);
             }
         }
-        if (ps < nseg) {
-            pj += kStageKeys;
-            if (pj >= L) {
-                pj = 0;
-                ps = next_live(ps + 1);
-            }
+        pj += kStageKeys;
+        if (pj >= L) {
+            pj = 0;
+            ps = next_live(ps + 1);
         }
     };
-#pragma unroll
-    for (int st = 0; st < kRingStages - 1; ++st) issue(st);
+    int total = 0;  // stages of the bundle
+    for (int k = 0; k < nseg; ++k) total += (seg_l(k) + kStageKeys - 1) / kStageKeys;
+    int issued = 0;
+    auto issue_next = [&]() {
+        issue(issued % kRingStages);
+        ++issued;
+    };
+    issue_next();
 
     // per-lane LDS offsets within a wave's stage: K rows as the A operand of S^T (row c, dims
     // 32 kk + 8 g ...), V rows for the transposing read (row 4g + c/4, 4 dims)
@@ -1045,14 +1054,18 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(DecodeParams p
     float mx = kEmpty, l = 0.f;
     f32x4_t acc[8];
     int cs = first_live, cj = 0, par = 0;
-    for (int t = 0; cs < nseg; ++t) {
-        issue((t + kRingStages - 1) % kRingStages);
+    for (int t = 0; t < total; ++t) {
+        if (issued < total) issue_next();  // the next stage, into the slot scored last
+        const int ahead = issued - 1 - t;  // stages issued after this one: 0 or 1
         const int L = seg_l(cs);
         const uint32_t hd = head_of(cs);
         if (cj == 0) {
             // a new request, while its first stage is in flight: its rows (loaded before every
             // ring stage) as B operands, columns c >= G zero
-            if (t == 0) wait_loads<kStageLoads * kRingStages>();
+            if (t == 0) {  // the rows were loaded before every stage
+                if (issued == 1) wait_loads<kStageLoads>();
+                else wait_loads<2 * kStageLoads>();
+            }
             const U4 zero = {0u, 0u, 0u, 0u};
             if constexpr (FUSED) {
                 // lane group r: query row r, lane c: chunk c; normalised, rotated, written back
@@ -1080,7 +1093,9 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(DecodeParams p
 #pragma unroll
             for (int db = 0; db < 8; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
         }
-        wait_loads<kStageLoads * (kRingStages - 1)>();  // this stage has landed
+        // this stage has landed (the next one stays in flight)
+        if (ahead == 0) wait_loads<0>();
+        else wait_loads<kStageLoads>();
         const uint32_t sb = lds_ring + (t % kRingStages) * kStageBytes + wave * kWaveStage;
         if constexpr (FUSED) {
             // the step's key and value enter the ring at row L-1 of the request's last stage
