@@ -110,6 +110,8 @@ __global__ void __launch_bounds__(256) prefill_rope_write_kernel(PrefillRopeWrit
 // units), so the accumulators are rescaled rarely and unnormalised weights stay below
 // 2^kRescaleLog2 (well inside bf16 and fp32 range).
 constexpr int kQBlock = 64;
+constexpr int kXcds = 8;        // MI355X: 8 XCDs of 32 CUs
+constexpr int kCusPerXcd = 32;
 constexpr int kTile = 32;     // keys per LDS stage and per softmax step
 constexpr int kStages = 3;    // LDS ring depth: loads run kStages - 1 tiles ahead
 constexpr float kLog2eP = 1.4426950408889634f;
@@ -192,9 +194,22 @@ prefill_attention_kernel(PrefillParams p) {
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, c = lane & 15;
     const int hgroups = p.Hq / GH;
-    const int hq0 = (blockIdx.x % hgroups) * GH;  // the workgroup's first query head
-    const int h = hq0 / p.group;                 // the workgroup's KV head
-    const int rest = blockIdx.x / hgroups;
+    // Placement: the hardware deals workgroup i to XCD i % 8 and, within an XCD, to its 32 CUs
+    // in turn, so CU k of an XCD holds the XCD's workgroups k, k + 32, k + 64 at once (three
+    // per CU).  Work items are numbered longest first; reversing the order within the second
+    // and third of every four rounds of 32 puts a short item next to every long one on a CU.
+    // Measured on the 16-prompt workload (seed 0): the most loaded CU from 27 to 20 tiles.
+    const int wg = [&] {
+        const int xcd = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
+        const int rounds = gridDim.x / (kXcds * kCusPerXcd);  // complete rounds on every XCD
+        if (j >= rounds * kCusPerXcd) return (int)blockIdx.x;
+        const int r = j / kCusPerXcd, pos = j % kCusPerXcd;
+        const bool flip = (r & 3) == 1 || (r & 3) == 2;
+        return (r * kCusPerXcd + (flip ? kCusPerXcd - 1 - pos : pos)) * kXcds + xcd;
+    }();
+    const int hq0 = (wg % hgroups) * GH;  // the workgroup's first query head
+    const int h = hq0 / p.group;          // the workgroup's KV head
+    const int rest = wg / hgroups;
     // Work item `rest` of this head group: a (64-query block qb, request b) pair, numbered with
     // the longest blocks first.  Up to 64 requests the numbering is dense: only pairs with
     // rows exist, so the grid's round-robin placement over shader engines sees real work
