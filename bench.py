@@ -425,6 +425,9 @@ def main():
     parser.add_argument("--grid", choices=["bundled", "balanced", "chunked"], default=None,
                         help="decode grid by name (default: the library's choice, bundled for "
                              "this workload)")
+    parser.add_argument("--no-plan", action="store_true",
+                        help="every layer launch ranks the requests itself instead of reading the "
+                             "step's decode plan")
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--calibrate-bytes", type=int, default=0,
@@ -466,10 +469,14 @@ def main():
                       row[..., (HQ + HKV) * D:].view(BATCH, 1, HKV, D),
                       arena[layer], arena[LAYERS + layer], out[layer]))
 
+    plan_buf = torch.empty(BATCH, 2, device=device, dtype=torch.int32)
+
     def step():
+        # one ranking per step (all layers attend the same lengths), inside the timed graph
+        plan = None if args.no_plan else pkg.decode_plan(positions, CAPACITY, out=plan_buf)
         for q, k, v, ak, av, o in views:
             pkg.decode_step(q, k, v, ak, av, positions, cos, sin, out=o, max_chunks=args.max_chunks,
-                            splits=args.splits, grid=args.grid)
+                            splits=args.splits, grid=args.grid, plan=plan)
 
     step()  # eager: sizes the workspace before capture
     torch.cuda.synchronize()
@@ -502,10 +509,11 @@ def main():
                          splits=args.splits, grid=args.grid)
     torch.cuda.synchronize()
     with torch.cuda.graph(attn_graph):
+        plan = None if args.no_plan else pkg.decode_plan(positions, CAPACITY, out=plan_buf)
         for layer in range(LAYERS):
             pkg.decode_attention(q0, arena[layer], arena[LAYERS + layer], positions,
                                  out=out[layer], max_chunks=args.max_chunks, splits=args.splits,
-                                 grid=args.grid)
+                                 grid=args.grid, plan=plan)
     attn_graph.replay()
     torch.cuda.synchronize()
     reps = max(1, args.steps // 4)
@@ -563,6 +571,7 @@ def main():
                    "us_per_layer_launch": launch_us,
                    "us_per_layer_attention_only": attn_us,
                    "attention_only_GBs": attention_bytes(contexts) / (attn_us * 1e-6) / 1e9,
+                   "decode_plan": not args.no_plan,
                    "max_chunks": args.max_chunks,
                    "splits": args.splits,
                    "wall_s_timed_region": wall,

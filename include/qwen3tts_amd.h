@@ -196,6 +196,11 @@ typedef struct q3t_decode_args {
     /* Q3T_GRID_AUTO (0), Q3T_GRID_CHUNKED, Q3T_GRID_BALANCED or Q3T_GRID_BUNDLED; a grid the
        call does not qualify for returns Q3T_EUNSUPPORTED */
     int64_t grid;
+    /* bundled grid, optional: the ranking q3t_decode_plan wrote for these `positions`, `batch`
+       and `ctx` (device, 2 * batch int32); the launch then skips its own ranking.  A plan made
+       for other positions gives wrong outputs (never accesses outside the arguments' ranges).
+       Ignored by the other grids; NULL = rank in the launch. */
+    const int32_t *plan;
 } q3t_decode_args;
 
 enum { Q3T_GRID_AUTO = 0, Q3T_GRID_CHUNKED = 1, Q3T_GRID_BALANCED = 2, Q3T_GRID_BUNDLED = 3 };
@@ -224,6 +229,16 @@ int q3t_decode_grid(const q3t_decode_args *args);
    allocating routine.  Every call on one GPU shares that GPU's array: calls that overlap in
    time on one GPU (on two streams) race. */
 int q3t_decode_attention_static(const q3t_decode_args *args, void *stream);
+
+/* The bundled grid's ranking of a step's requests, written once per step and passed as
+   `plan` to every layer's launch of that step (the talker's layers all attend the same
+   lengths): plan[2r], plan[2r + 1] = b, L_b for the request b of rank r, with L_b =
+   positions[b] + 1 for a position in [0, ctx) and 0 otherwise, ranked by L_b descending, ties
+   by ascending b.  batch <= 128, ctx <= 2^20; `plan` holds 2 * batch int32 (8-byte aligned).
+   One small kernel on `stream`; it may be captured.  No counterpart in the reference (its
+   attention operator takes no per-step state; positions are fixed for a step's layers in
+   SlotGraph.compute, continuous.py:188-198). */
+int q3t_decode_plan(const int64_t *positions, int64_t batch, int64_t ctx, int32_t *plan, void *stream);
 
 /* Re-zero the counter region of a decode workspace on `stream` (a kernel, so it may be
    captured).  Every completed launch leaves the counters zeroed; a launch that failed

@@ -8,7 +8,8 @@ Modules
   packed_kv       copy_packed_prefix                     (packed_kv.py)
   kv_write        write / write_tokens                   (kv_triton_ascend.py, SlotCache.update)
   rotary          rotary / rope_tables                   (rotary_triton_ascend.py, rotary_emb)
-  attention       attention / decode_attention / decode_step / decode_grid_for / prefill_attention
+  attention       attention / decode_attention / decode_step / decode_plan / decode_grid_for /
+                  prefill_attention
                                                          (npu_attention.py, SDPA dispatch)
   slots           SlotArena / SlotCache / PredictorCache (continuous.py, predictor.py)
   packed_attention PackedAttention / install_packed_attention / restore_modules
@@ -23,7 +24,8 @@ from .batching import decode_batch_size
 from .packed_kv import copy_packed_prefix, copy_rows
 from .kv_write import write, write_tokens
 from .rotary import rotary, rope_tables, inverse_frequencies
-from .attention import attention, decode_attention, decode_step, decode_grid_for, prefill_attention
+from .attention import (attention, decode_attention, decode_step, decode_grid_for, decode_plan,
+                        prefill_attention)
 from .prefill import prefill_rope_write, prefill_step
 from .packed_attention import PackedAttention, install_packed_attention, restore_modules
 from .scheduler import SlotScheduler, DecodeBatch
@@ -34,6 +36,7 @@ from .prefill_graph import PrefillGraph, pad_prefill_batch
 __all__ = [
     "decode_batch_size", "copy_packed_prefix", "copy_rows", "write", "write_tokens", "rotary",
     "rope_tables", "inverse_frequencies", "attention", "decode_attention", "decode_step", "decode_grid_for",
+    "decode_plan",
     "prefill_attention", "prefill_rope_write", "prefill_step", "PackedAttention",
     "install_packed_attention", "restore_modules", "SlotScheduler", "DecodeBatch", "SlotArena",
     "SlotCache", "PredictorCache", "PrefillCache", "grow_arena", "SlotGraph", "PrefillGraph",

@@ -50,6 +50,7 @@ class DecodeArgs(ctypes.Structure):
         ("nk_stride_s", c_i64), ("nv_stride_s", c_i64), ("cs_stride_s", c_i64),
         ("splits", c_i64),
         ("grid", c_i64),
+        ("plan", c_vp),
     ]
 
 
@@ -102,6 +103,7 @@ SIGNATURES = {
     "q3t_decode_grid": (ctypes.c_int, [ctypes.POINTER(DecodeArgs)]),
     "q3t_decode_attention": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
     "q3t_decode_reset_workspace": (ctypes.c_int, [c_vp, c_i64, c_vp]),
+    "q3t_decode_plan": (ctypes.c_int, [c_vp, c_i64, c_i64, c_vp, c_vp]),
     "q3t_decode_attention_static": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
     "q3t_prefill_attention": (ctypes.c_int, [ctypes.POINTER(PrefillArgs), c_vp]),
     "q3t_prefill_rope_write": (ctypes.c_int, [ctypes.POINTER(PrefillRopeWriteArgs), c_vp]),
@@ -115,7 +117,7 @@ class KernelError(RuntimeError):
     """A HIP launch failed after host validation passed."""
 
 
-ABI_VERSION = 5  # q3t_abi_version() of the header these structures mirror
+ABI_VERSION = 6  # q3t_abi_version() of the header these structures mirror
 
 
 def library() -> ctypes.CDLL:

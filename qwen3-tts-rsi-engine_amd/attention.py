@@ -132,8 +132,53 @@ def decode_grid_for(batch, query_len, q_heads, kv_heads, head_dim, ctx, dtype=to
     return {v: k for k, v in GRIDS.items() if k not in (None, 'auto')}[code]
 
 
+PLAN_MAX_BATCH = 128  # requests a decode plan ranks (the bundled grid's limit)
+
+
+def decode_plan(positions, capacity, *, out=None):
+    """The bundled grid's ranking of a step's requests, made once for the step's positions
+    and passed as ``plan=`` to every layer's ``decode_step`` / ``decode_attention`` of that step
+    (the layers of a talker step all attend the same lengths, SlotGraph.compute,
+    continuous.py:188-198), so that no launch ranks the requests itself.  positions (B,) int64
+    with B <= 128, capacity: the arena's rows (the launches' ctx).  Returns an int32 (B, 2)
+    tensor of (request, keys) pairs, longest first (ties by request index); a request without
+    a position in [0, capacity) has 0 keys.  One small kernel on the current stream (it can be
+    captured); the plan stays valid while ``positions`` and ``capacity`` are unchanged: a plan
+    of other positions gives wrong outputs."""
+    if positions.ndim != 1 or positions.dtype != torch.int64:
+        raise ValueError('positions must be an int64 (batch,) tensor')
+    batch = positions.shape[0]
+    if batch > PLAN_MAX_BATCH:
+        raise ValueError(f'a decode plan ranks at most {PLAN_MAX_BATCH} requests')
+    if not 1 <= int(capacity) <= 1 << 20:
+        raise ValueError('capacity must be in [1, 2^20]')
+    device = _lib.require_gpu(positions)
+    if not positions.is_contiguous():
+        positions = positions.contiguous()
+    if out is None:
+        out = torch.empty(batch, 2, device=device, dtype=torch.int32)
+    else:
+        _check_out(out, (batch, 2), torch.int32, device, 'decode plan')
+        if not out.is_contiguous():
+            raise ValueError('decode plan: out must be contiguous')
+    with torch.cuda.device(device):
+        status = _lib.library().q3t_decode_plan(positions.data_ptr(), batch, int(capacity), out.data_ptr(),
+                                                _lib.stream_handle(device))
+    _lib.check(status, 'decode plan')
+    return out
+
+
+def _set_plan(a, plan, batch, device):
+    if plan is None:
+        return
+    if (plan.shape != (batch, 2) or plan.dtype != torch.int32 or not plan.is_contiguous()
+            or plan.device != device):
+        raise ValueError(f'plan must be the contiguous int32 ({batch}, 2) tensor of decode_plan on {device}')
+    a.plan = plan.data_ptr()
+
+
 def decode_attention(query, keys, values, positions, *, scale=None, mask=None, kv_offsets=None,
-                     out=None, max_chunks=0, splits=0, grid=None, no_alloc=False):
+                     out=None, max_chunks=0, splits=0, grid=None, no_alloc=False, plan=None):
     """query (B, S, Hq, D) BSND; keys/values (B, Hkv, ctx, D) views of the arena (or, with
     ``kv_offsets``, any base tensor whose request rows start at those element offsets);
     positions (B,) int64: the last query position of each request.  ``grid`` picks the
@@ -144,7 +189,9 @@ def decode_attention(query, keys, values, positions, *, scale=None, mask=None, k
     ~512 workgroups) or None for the library's choice, in which ``splits`` > 0 / < 0 still
     selects balanced / chunked.  ``no_alloc`` runs the library's allocation-free entry point, which keeps
     its split states in a fixed per-GPU device array instead of a workspace (calls that
-    overlap in time on one GPU then race).  Returns (B, S, Hq, D)."""
+    overlap in time on one GPU then race).  ``plan``: ``decode_plan(positions, ctx)`` of these
+    positions; the bundled grid then skips its own ranking (other grids ignore it).
+    Returns (B, S, Hq, D)."""
     if query.ndim != 4 or keys.ndim != 4 or values.shape != keys.shape:
         raise ValueError('expected BSND query and BNSD key/value views')
     batch, qlen, q_heads, head_dim = query.shape
@@ -191,13 +238,14 @@ def decode_attention(query, keys, values, positions, *, scale=None, mask=None, k
     a.max_chunks = int(max_chunks)
     a.splits = int(splits)
     a.grid = _grid_code(grid)
+    _set_plan(a, plan, batch, device)
     _run_decode(a, device, 'decode attention', no_alloc)
     return out
 
 
 def decode_step(query, new_key, new_value, key_arena, value_arena, positions, cos, sin, *,
                 scale=None, out=None, max_chunks=0, splits=0, grid=None, q_norm_weight=None,
-                k_norm_weight=None, norm_eps=1e-6, mask=None, no_alloc=False):
+                k_norm_weight=None, norm_eps=1e-6, mask=None, no_alloc=False, plan=None):
     """Fused decode step of a layer for one token, or two (the code predictor's first step).
 
     query (B, S, Hq, D), new_key/new_value (B, S, Hkv, D) with S in {1, 2}: un-rotated bf16
@@ -215,8 +263,8 @@ def decode_step(query, new_key, new_value, key_arena, value_arena, positions, co
     ``mask`` (SDPA-style, broadcastable to (B, 1, S, C)) is added to the scores of the keys
     0 ... positions[b], as the reference's operator applies the mask it is given; without it
     request b attends exactly those keys (the ``j <= pos[b]`` mask of SlotGraph.compute).
-    ``grid`` / ``splits`` / ``max_chunks`` choose the grid and ``no_alloc`` the
-    allocation-free entry point, as in ``decode_attention``."""
+    ``grid`` / ``splits`` / ``max_chunks`` choose the grid, ``no_alloc`` the
+    allocation-free entry point and ``plan`` the step's ranking, as in ``decode_attention``."""
     if (query.ndim != 4 or query.shape[1] not in (1, 2) or new_key.ndim != 4
             or new_key.shape[1] != query.shape[1]):
         raise ValueError('fused decode expects one- or two-token BSND rows')
@@ -287,6 +335,7 @@ def decode_step(query, new_key, new_value, key_arena, value_arena, positions, co
         _lib.require_gpu(weight)
         setattr(a, name, weight.data_ptr())
     a.norm_eps = float(norm_eps)
+    _set_plan(a, plan, batch, device)
     _run_decode(a, device, 'fused decode step', no_alloc)
     return out
 

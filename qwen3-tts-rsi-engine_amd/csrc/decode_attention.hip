@@ -68,6 +68,7 @@ struct DecodeParams {
     float eps;
     int stream;             // read K/V rows with the non-temporal cache policy (host choice)
     int64_t nk_ss, nv_ss, cs_ss;  // fused, two tokens: token strides of new K/V and cos/sin
+    const int32_t *plan;    // bundled grid, optional: (b, L) pairs ranked longest first
 };
 
 Q3T_DEVICE int mask_elem_size(int dtype) { return dtype == Q3T_F32 ? 4 : dtype == Q3T_BOOL ? 1 : 2; }
@@ -859,11 +860,11 @@ constexpr float kRescaleLog2 = 8.0f;  // the running maximum moves when exceeded
 template <int G>
 struct BundleLds {
     char ring[kRingStages][kStageBytes];
-    // per wave and request: rows 0..G-1 query, 4 cos, 5 sin, 6 new K, 7 new V
-    char head[kWaves][kBundleMaxSeg][8][kRowBytes];
+    // per request (shared by the waves): rows 0..G-1 query, 4 cos, 5 sin, 6 new K, 7 new V
+    char head[kBundleMaxSeg][8][kRowBytes];
     float acc[2][kWaves][G][128];
     float ml[2][kWaves][G][2];
-    uint16_t outq[kBundleMaxSeg][G][128];  // bf16 outputs, stored after the stream
+    alignas(16) uint16_t outq[kBundleMaxSeg][G][128];  // bf16 outputs, stored after the stream
     alignas(16) int keys[kWaves][kBundleMaxBatch];  // each wave's copy of the ranking keys
 };
 
@@ -887,7 +888,9 @@ template <int G, bool FUSED, bool STREAM>
 __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(DecodeParams p) {
     static_assert(G >= 1 && G <= 4, "query rows are the first G of 16 MFMA columns, four LDS rows");
     __shared__ __attribute__((aligned(16))) BundleLds<G> s;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c = lane & 15;
+    prefetch_kernargs<sizeof(DecodeParams)>();
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS bases stay scalar
     const int h = blockIdx.x % p.Hkv, m = blockIdx.x / p.Hkv, M = p.bundles;
 
     // weights of the fused norms (chunk c of the row), loaded with the positions and waited for
@@ -898,49 +901,82 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(DecodeParams p
         if (p.qnw) qw = load16(p.qnw + c * 16);
         if (p.knw) kw = load16(p.knw + c * 16);
     }
-    // ranks: key = L * 1024 + (1023 - b) (longest first, ties by index; L = 0 without a valid
-    // position).  Lane holds requests lane and lane + 64; each wave ranks in its own LDS copy
-    // of the keys (no barrier), reading four keys per load.
-    int key[2], len[2];
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const int b = lane + 64 * e;
-        int L = 0;
-        if (b < p.B) {
-            const int64_t pb = p.pos[b];
-            L = (pb >= 0 && pb < p.ctx) ? (int)pb + 1 : 0;
-        }
-        len[e] = L;
-        key[e] = b < p.B ? (L << 10) | (1023 - b) : -1;
-        s.keys[wave][b] = key[e];
-    }
-    asm volatile("" :: "v"(qw.x), "v"(kw.x) : "memory");
-    const int nb4 = (p.B + 3) >> 2;
-    int rank[2] = {0, 0};
-    for (int u = 0; u < nb4; ++u) {
-        const i32x4_t k4 = *(const i32x4_t *)&s.keys[wave][4 * u];  // keys past B are -1
-#pragma unroll
-        for (int e = 0; e < 2; ++e)
-            rank[e] += (k4.x > key[e]) + (k4.y > key[e]) + (k4.z > key[e]) + (k4.w > key[e]);
-    }
-    // the bundle's requests: ranks m, 2M-1-m, 2M+m, 4M-1-m below B
-    Slots4<int> tb_b = {0, 0, 0, 0}, tb_l = {0, 0, 0, 0};
+    // The bundle's requests are those of ranks m, 2M-1-m, 2M+m, 4M-1-m below B (rank 0 the
+    // longest, ties by index).  Request slot k of the bundle: b (-1: none), length L (0: attends
+    // nothing) and the row-0 element offsets of its K and V rows.
+    Slots4<int> tb_b = {-1, -1, -1, -1}, tb_l = {0, 0, 0, 0};
     Slots4<int64_t> tb_k = {0, 0, 0, 0}, tb_v = {0, 0, 0, 0};
     int nseg = 0;
-#pragma unroll
-    for (int i = 0; i < kBundleMaxSeg; ++i) {
-        const int r = (i >> 1) * 2 * M + ((i & 1) ? 2 * M - 1 - m : m);
-        if (r >= p.B) continue;
-        const uint64_t m0 = __builtin_amdgcn_ballot_w64(rank[0] == r && lane < p.B);
-        const uint64_t m1 = __builtin_amdgcn_ballot_w64(rank[1] == r && lane + 64 < p.B);
-        const int b = m0 ? (int)__builtin_ctzll(m0) : 64 + (int)__builtin_ctzll(m1);
-        const int L = m0 ? __builtin_amdgcn_readlane(len[0], b) : __builtin_amdgcn_readlane(len[1], b - 64);
-        const int64_t o = p.offs ? p.offs[b] : 0;
+    auto bundle_rank = [&](int i) { return (i >> 1) * 2 * M + ((i & 1) ? 2 * M - 1 - m : m); };
+    auto set_slot = [&](int i, int b, int L) {
+        const int64_t o = p.offs && b >= 0 ? p.offs[b] : 0;
         tb_b.set(i, b);
         tb_l.set(i, L);
         tb_k.set(i, (p.offs ? o : (int64_t)b * p.k_sb) + h * p.k_sh);
         tb_v.set(i, (p.offs ? o : (int64_t)b * p.v_sb) + h * p.v_sh);
         nseg = i + 1;
+    };
+    if (p.plan) {
+        // a ranking made once for the step's positions (q3t_decode_plan): (b, L) pairs, longest
+        // first.  One wave-uniform load round trip and no ranking here; entries that do not
+        // name a request of this batch attend nothing and write nothing.
+        // The four entries come in one scalar round trip (ranks past the batch read entry 0 and
+        // are ignored); written out, the compiler serialised them as vector loads.
+        const uint64_t base = reinterpret_cast<uint64_t>(p.plan);
+        uint64_t a[kBundleMaxSeg], e[kBundleMaxSeg];
+#pragma unroll
+        for (int i = 0; i < kBundleMaxSeg; ++i)
+            a[i] = base + 8 * (uint64_t)(bundle_rank(i) < p.B ? bundle_rank(i) : 0);
+        asm volatile("s_load_dwordx2 %0, %4, 0x0\n\ts_load_dwordx2 %1, %5, 0x0\n\t"
+                     "s_load_dwordx2 %2, %6, 0x0\n\ts_load_dwordx2 %3, %7, 0x0\n\ts_waitcnt lgkmcnt(0)"
+                     : "=&s"(e[0]), "=&s"(e[1]), "=&s"(e[2]), "=&s"(e[3])
+                     : "s"(a[0]), "s"(a[1]), "s"(a[2]), "s"(a[3]) : "memory");
+#pragma unroll
+        for (int i = 0; i < kBundleMaxSeg; ++i) {
+            if (bundle_rank(i) >= p.B) continue;
+            const int b = (int)(uint32_t)e[i], L = (int)(uint32_t)(e[i] >> 32);
+            const bool ok = b >= 0 && b < p.B;
+            set_slot(i, ok ? b : -1, ok ? min(max(L, 0), p.ctx) : 0);
+        }
+        asm volatile("" :: "v"(qw.x), "v"(kw.x) : "memory");
+    } else {
+        // ranks: key = L * 1024 + (1023 - b) (longest first, ties by index; L = 0 without a
+        // valid position).  Lane holds requests lane and lane + 64; each wave ranks in its own
+        // LDS copy of the keys (no barrier), reading eight 16-byte groups of keys per wait.
+        int key[2], len[2];
+        int64_t pb[2] = {-1, -1};
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+            if (lane + 64 * e < p.B) pb[e] = p.pos[lane + 64 * e];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int b = lane + 64 * e;
+            const int L = (pb[e] >= 0 && pb[e] < p.ctx) ? (int)pb[e] + 1 : 0;
+            len[e] = L;
+            key[e] = b < p.B ? (L << 10) | (1023 - b) : -1;
+            s.keys[wave][b] = key[e];
+        }
+        asm volatile("" :: "v"(qw.x), "v"(kw.x) : "memory");
+        int rank[2] = {0, 0};
+        for (int u0 = 0; u0 < p.B; u0 += 32) {  // keys past B are -1
+            i32x4_t k4[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) k4[j] = *(const i32x4_t *)&s.keys[wave][u0 + 4 * j];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+                    rank[e] += (k4[j].x > key[e]) + (k4[j].y > key[e]) + (k4[j].z > key[e]) + (k4[j].w > key[e]);
+        }
+#pragma unroll
+        for (int i = 0; i < kBundleMaxSeg; ++i) {
+            const int r = bundle_rank(i);
+            if (r >= p.B) continue;
+            const uint64_t m0 = __builtin_amdgcn_ballot_w64(rank[0] == r && lane < p.B);
+            const uint64_t m1 = __builtin_amdgcn_ballot_w64(rank[1] == r && lane + 64 < p.B);
+            const int b = m0 ? (int)__builtin_ctzll(m0) : 64 + (int)__builtin_ctzll(m1);
+            set_slot(i, b, m0 ? __builtin_amdgcn_readlane(len[0], b) : __builtin_amdgcn_readlane(len[1], b - 64));
+        }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // offsets loaded before any ring load
 
@@ -958,6 +994,7 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(DecodeParams p
         if (wave == 0) {
             for (int k = 0; k < nseg; ++k) {
                 const int b = seg_b(k);
+                if (b < 0) continue;
                 for (int t = lane; t < G * 128; t += 64)
                     store_out<uint16_t>(p.out + (b * p.o_sb + (h * G + t / 128) * p.o_sh + t % 128) * 2, 0.f);
             }
@@ -968,48 +1005,28 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(DecodeParams p
     const int kst = (int)(p.k_st * 2), vst = (int)(p.v_st * 2);
     const uint32_t kbytes = (uint32_t)((p.ctx - 1) * kst + kRowBytes), vbytes = (uint32_t)((p.ctx - 1) * vst + kRowBytes);
     const uint32_t lds_ring = (uint32_t)(uintptr_t)&s.ring[0][0];
-    auto head_of = [&](int k) { return (uint32_t)(uintptr_t)&s.head[wave][k][0][0]; };
+    auto head_of = [&](int k) { return (uint32_t)(uintptr_t)&s.head[k][0][0]; };
 
-    // this wave's rows of every request of the bundle, ahead of the ring
-    for (int k = 0; k < nseg; ++k) {
-        const int b = seg_b(k);
-        if (seg_l(k) == 0) continue;
-        const uint32_t hd = (uint32_t)__builtin_amdgcn_readfirstlane((int)head_of(k));
-        const i32x4_t qrs = scalar_rsrc(p.q + (b * p.q_sb + (int64_t)h * G * p.q_sh) * 2,
-                                        (uint32_t)((G - 1) * p.q_sh * 2 + kRowBytes));
-        if (lane < 16 * G) load_to_lds16(qrs, (uint32_t)((lane >> 4) * p.q_sh * 2 + (lane & 15) * 16), hd);
-        if constexpr (FUSED) {
-            const i32x4_t crs = scalar_rsrc(p.cs + b * p.cs_sb * 2, kRowBytes);
-            const i32x4_t srs = scalar_rsrc(p.sn + b * p.cs_sb * 2, kRowBytes);
-            const i32x4_t nkr = scalar_rsrc(p.nk + (b * p.nk_sb + h * p.nk_sh) * 2, kRowBytes);
-            const i32x4_t nvr = scalar_rsrc(p.nv + (b * p.nv_sb + h * p.nv_sh) * 2, kRowBytes);
-            if (lane < 16) {
-                load_to_lds16(crs, lane * 16, hd + 4 * kRowBytes);
-                load_to_lds16(srs, lane * 16, hd + 5 * kRowBytes);
-            }
-            // the step's key and value only in the wave that attends row L-1
-            if (lane < 16 && wave == ((seg_l(k) - 1) % kStageKeys) / kWaveKeys) {
-                load_to_lds16(nkr, lane * 16, hd + 6 * kRowBytes);
-                load_to_lds16(nvr, lane * 16, hd + 7 * kRowBytes);
-            }
-        }
-    }
-
-    // producer: the next stage to load (request index ps, first key pj); rows at or past the
-    // request's keys get offsets outside the resource (zeros, no memory access)
-    int ps = first_live, pj = 0;
+    // producer: the next stage to load (request slot ps, first key pj); rows at or past the
+    // request's keys get offsets outside the resource (zeros, no memory access).  The request's
+    // resources and key counts stay in scalar registers from one stage to the next.
+    int ps = first_live, pj = 0, pL = 0, pjend = 0;
+    i32x4_t krs, vrs;
+    auto producer_request = [&]() {
+        pL = seg_l(ps);
+        pjend = FUSED ? pL - 1 : pL;  // fused: row L-1 is the step's own key
+        krs = scalar_rsrc(seg_row0(p.k, tb_k, ps), kbytes);
+        vrs = scalar_rsrc(seg_row0(p.v, tb_v, ps), vbytes);
+    };
+    producer_request();
+    // No wait for this wave's earlier reads of the slot: every one of them fed a product (or,
+    // for the step's key, preceded such reads of the same wave), so all have returned.
     auto issue = [&](int slot) {
-        const int kq = ps;
-        const int L = seg_l(ps);
-        const int jend = FUSED ? L - 1 : L;  // fused: row L-1 is the step's own key
-        const i32x4_t krs = scalar_rsrc(seg_row0(p.k, tb_k, kq), kbytes);
-        const i32x4_t vrs = scalar_rsrc(seg_row0(p.v, tb_v, kq), vbytes);
         const uint32_t base = lds_ring + slot * kStageBytes + wave * kWaveStage;
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this slot's last reads have returned
 #pragma unroll
         for (int i = 0; i < kWaveKeys / 4; ++i) {
             const int r = 4 * i + g, j = pj + wave * kWaveKeys + r;
-            const bool ok = j < jend;
+            const bool ok = j < pjend;
             const uint32_t ko = ok ? (uint32_t)(j * kst + ((c ^ r) & 15) * 16) : 0xfffffff0u;
             const uint32_t vo = ok ? (uint32_t)(j * vst + ((c ^ (2 * r)) & 15) * 16) : 0xfffffff0u;
             const uint32_t kl = (uint32_t)__builtin_amdgcn_readfirstlane((int)(base + i * 1024));
@@ -1023,19 +1040,49 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(DecodeParams p
             }
         }
         pj += kStageKeys;
-        if (pj >= L) {
+        if (pj >= pL) {
             pj = 0;
             ps = next_live(ps + 1);
+            if (ps < nseg) producer_request();
         }
     };
     int total = 0;  // stages of the bundle
-    for (int k = 0; k < nseg; ++k) total += (seg_l(k) + kStageKeys - 1) / kStageKeys;
+#pragma unroll
+    for (int k = 0; k < kBundleMaxSeg; ++k)
+        if (k < nseg) total += (tb_l.get(k) + kStageKeys - 1) / kStageKeys;
     int issued = 0;
     auto issue_next = [&]() {
         issue(issued % kRingStages);
         ++issued;
     };
+    // The rows of every request of the bundle (query rows; fused: cos/sin and the step's key
+    // and value) go out first, request k's from wave k % 4, then the ring's first two stages:
+    // the rows land first, so each request's rotations happen once, in its own wave, while the
+    // stages are in flight.  The slots are unrolled so that the bundle table is read without
+    // branches.
+#pragma unroll
+    for (int k = 0; k < kBundleMaxSeg; ++k) {
+        if (k >= nseg || tb_l.get(k) == 0 || wave != k % kWaves) continue;
+        const int b = tb_b.get(k);
+        const uint32_t hd = (uint32_t)__builtin_amdgcn_readfirstlane((int)head_of(k));
+        const i32x4_t qrs = scalar_rsrc(p.q + (b * p.q_sb + (int64_t)h * G * p.q_sh) * 2,
+                                        (uint32_t)((G - 1) * p.q_sh * 2 + kRowBytes));
+        if (lane < 16 * G) load_to_lds16(qrs, (uint32_t)((lane >> 4) * p.q_sh * 2 + (lane & 15) * 16), hd);
+        if constexpr (FUSED) {
+            const i32x4_t crs = scalar_rsrc(p.cs + b * p.cs_sb * 2, kRowBytes);
+            const i32x4_t srs = scalar_rsrc(p.sn + b * p.cs_sb * 2, kRowBytes);
+            const i32x4_t nkr = scalar_rsrc(p.nk + (b * p.nk_sb + h * p.nk_sh) * 2, kRowBytes);
+            const i32x4_t nvr = scalar_rsrc(p.nv + (b * p.nv_sb + h * p.nv_sh) * 2, kRowBytes);
+            if (lane < 16) {
+                load_to_lds16(crs, lane * 16, hd + 4 * kRowBytes);
+                load_to_lds16(srs, lane * 16, hd + 5 * kRowBytes);
+                load_to_lds16(nkr, lane * 16, hd + 6 * kRowBytes);
+                load_to_lds16(nvr, lane * 16, hd + 7 * kRowBytes);
+            }
+        }
+    }
     issue_next();
+    if (issued < total) issue_next();
 
     // per-lane LDS offsets within a wave's stage: K rows as the A operand of S^T (row c, dims
     // 32 kk + 8 g ...), V rows for the transposing read (row 4g + c/4, 4 dims)
@@ -1054,34 +1101,44 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(DecodeParams p
     float mx = kEmpty, l = 0.f;
     f32x4_t acc[8];
     int cs = first_live, cj = 0, par = 0;
+    int L = seg_l(cs);  // the consumer's request: its keys and rows, kept between stages
+    uint32_t hd = head_of(cs);
     for (int t = 0; t < total; ++t) {
-        if (issued < total) issue_next();  // the next stage, into the slot scored last
+        // the next stage, into the slot scored last (the first two went out before the loop)
+        if (issued < total && issued <= t + 1) issue_next();
         const int ahead = issued - 1 - t;  // stages issued after this one: 0 or 1
-        const int L = seg_l(cs);
-        const uint32_t hd = head_of(cs);
-        if (cj == 0) {
-            // a new request, while its first stage is in flight: its rows (loaded before every
-            // ring stage) as B operands, columns c >= G zero
-            if (t == 0) {  // the rows were loaded before every stage
-                if (issued == 1) wait_loads<kStageLoads>();
-                else wait_loads<2 * kStageLoads>();
-            }
-            const U4 zero = {0u, 0u, 0u, 0u};
+        if (t == 0) {
+            // the rows landed before the stages (which stay in flight)
+            if (issued == 1) wait_loads<kStageLoads>();
+            else wait_loads<2 * kStageLoads>();
             if constexpr (FUSED) {
-                // lane group r: query row r, lane c: chunk c; normalised, rotated, written back
-                const U4 cv = lds_read16(hd + 4 * kRowBytes + c * 16), sv = lds_read16(hd + 5 * kRowBytes + c * 16);
-                U4 x = lds_read16(hd + g * kRowBytes + c * 16);
-                if (p.qnw) x = rms_norm8<16>(x, qw, p.eps, 128);
-                x = rope_half8(x, xor8_u4(x), cv, sv, c < 8);
-                if (g < G) lds_write16(hd + g * kRowBytes + c * 16, x);
-                // the step's key, in the wave that attends row L-1: rotated, kept in row 6
-                if (wave == ((L - 1) % kStageKeys) / kWaveKeys) {
-                    U4 kx = lds_read16(hd + 6 * kRowBytes + c * 16);
-                    if (p.knw) kx = rms_norm8<16>(kx, kw, p.eps, 128);
-                    kx = rope_half8(kx, xor8_u4(kx), cv, sv, c < 8);
-                    if (g == 0) lds_write16(hd + 6 * kRowBytes + c * 16, kx);
+                // each request's rows in the wave that loaded them, while the first stages are in
+                // flight: lane group r < G holds query row r and lane group G the step's key (a
+                // second pass for G = 4), lane c chunk c; normalised, rotated and written back
+#pragma unroll
+                for (int k = 0; k < kBundleMaxSeg; ++k) {
+                    if (k >= nseg || tb_l.get(k) == 0 || wave != k % kWaves) continue;
+                    const int Lk = tb_l.get(k);
+                    const uint32_t hk = head_of(k);
+                    const U4 cv = lds_read16(hk + 4 * kRowBytes + c * 16), sv = lds_read16(hk + 5 * kRowBytes + c * 16);
+                    auto rotate = [&](int row, bool is_key) {
+                        U4 x = lds_read16(hk + row * kRowBytes + c * 16);
+                        if (is_key ? p.knw != nullptr : p.qnw != nullptr) x = rms_norm8<16>(x, is_key ? kw : qw, p.eps, 128);
+                        return rope_half8(x, xor8_u4(x), cv, sv, c < 8);
+                    };
+                    if constexpr (G < 4) {
+                        if (g <= G) lds_write16(hk + (g < G ? g : 6) * kRowBytes + c * 16, rotate(g < G ? g : 6, g == G));
+                    } else {
+                        lds_write16(hk + g * kRowBytes + c * 16, rotate(g, false));
+                        if (g == 0) lds_write16(hk + 6 * kRowBytes + c * 16, rotate(6, true));
+                    }
                 }
             }
+            lds_barrier();  // every request's rows, rotated, visible to every wave
+        }
+        if (cj == 0) {
+            // a new request: its rows as B operands, columns c >= G zero
+            const U4 zero = {0u, 0u, 0u, 0u};
             const int cq = c < G ? c : 0;
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
@@ -1096,6 +1153,25 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(DecodeParams p
         // this stage has landed (the next one stays in flight)
         if (ahead == 0) wait_loads<0>();
         else wait_loads<kStageLoads>();
+        if constexpr (FUSED) {
+            if (t == 0) {
+                // the step's keys and values into the arena, by each request's wave, only now: a
+                // store shares the load counter, so one issued before this wait would have held it
+                // up until part of the next stage had landed as well
+#pragma unroll
+                for (int k = 0; k < kBundleMaxSeg; ++k) {
+                    if (k >= nseg || tb_l.get(k) == 0 || wave != k % kWaves) continue;
+                    if (g == 0) {
+                        const int Lk = tb_l.get(k);
+                        const uint32_t hk = head_of(k);
+                        const auto krs = buffer_rsrc(uniform_ptr(seg_row0(p.k, tb_k, k)), kbytes);
+                        const auto vrs = buffer_rsrc(uniform_ptr(seg_row0(p.v, tb_v, k)), vbytes);
+                        buffer_store16(krs, (uint32_t)((Lk - 1) * kst + c * 16), lds_read16(hk + 6 * kRowBytes + c * 16));
+                        buffer_store16(vrs, (uint32_t)((Lk - 1) * vst + c * 16), lds_read16(hk + 7 * kRowBytes + c * 16));
+                    }
+                }
+            }
+        }
         const uint32_t sb = lds_ring + (t % kRingStages) * kStageBytes + wave * kWaveStage;
         if constexpr (FUSED) {
             // the step's key and value enter the ring at row L-1 of the request's last stage
@@ -1174,32 +1250,69 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(DecodeParams p
             par ^= 1;
             cs = next_live(cs + 1);
             cj = 0;
-        }
-    }
-    // stores only now: a store shares the load counter, so one issued during the stream would
-    // hold up the next ring wait until it completed.  Output rows (zeros for requests without a
-    // valid position); fused, the step's key and value rows at L-1 from the wave that rotated
-    // the key (nothing in this launch reads them from the arena).
-    lds_barrier();
-    for (int k = 0; k < nseg; ++k) {
-        const int b = seg_b(k);
-        const int L = seg_l(k);
-        for (int t = tid; t < G * 128; t += kThreads) {
-            const int cc = t / 128, d = t % 128;
-            *reinterpret_cast<uint16_t *>(p.out + (b * p.o_sb + (h * G + cc) * p.o_sh + d) * 2) =
-                L > 0 ? s.outq[k][cc][d] : (uint16_t)0;
-        }
-        if constexpr (FUSED) {
-            if (L > 0 && wave == ((L - 1) % kStageKeys) / kWaveKeys && g == 0) {
-                const uint32_t hd = head_of(k);
-                const auto krs = buffer_rsrc(uniform_ptr(seg_row0(p.k, tb_k, k)), kbytes);
-                const auto vrs = buffer_rsrc(uniform_ptr(seg_row0(p.v, tb_v, k)), vbytes);
-                buffer_store16(krs, (uint32_t)((L - 1) * kst + c * 16), lds_read16(hd + 6 * kRowBytes + c * 16));
-                buffer_store16(vrs, (uint32_t)((L - 1) * vst + c * 16), lds_read16(hd + 7 * kRowBytes + c * 16));
+            if (cs < nseg) {
+                L = seg_l(cs);
+                hd = head_of(cs);
             }
         }
     }
-    wait_loads<0>();  // the trailing ring loads land before the workgroup's LDS is released
+    // Output rows (zeros for requests without a valid position) once every request is merged.
+    // No load is outstanding here (every stage was awaited), so the workgroup ends without
+    // waiting for its stores.
+    // 16-byte stores (one lane per 8 elements) when the output rows allow them, else 2-byte ones.
+    lds_barrier();
+    const bool vec_out = ((reinterpret_cast<uintptr_t>(p.out) | (uintptr_t)(p.o_sb * 2) | (uintptr_t)(p.o_sh * 2)) & 15) == 0;
+#pragma unroll
+    for (int k = 0; k < kBundleMaxSeg; ++k) {
+        if (k >= nseg) continue;
+        const int b = tb_b.get(k);
+        const int L = tb_l.get(k);
+        if (b < 0) continue;
+        if (vec_out) {
+            if (tid < G * 16) {
+                const int cc = tid / 16, ch = tid % 16;
+                const U4 v = L > 0 ? *reinterpret_cast<const U4 *>(&s.outq[k][cc][ch * 8]) : U4{0u, 0u, 0u, 0u};
+                store16(p.out + (b * p.o_sb + (h * G + cc) * p.o_sh + ch * 8) * 2, v);
+            }
+        } else {
+            for (int t = tid; t < G * 128; t += kThreads) {
+                const int cc = t / 128, d = t % 128;
+                *reinterpret_cast<uint16_t *>(p.out + (b * p.o_sb + (h * G + cc) * p.o_sh + d) * 2) =
+                    L > 0 ? s.outq[k][cc][d] : (uint16_t)0;
+            }
+        }
+    }
+}
+
+// The ranking the bundled grid works from, made once for a step's positions and read by every
+// layer's launch of that step (all layers of a talker step attend the same lengths): plan[r] =
+// (b, L_b) for the request b of rank r, L_b = pos[b] + 1 for a position in [0, ctx) and 0
+// otherwise, ranked by L descending with ties by ascending b.  One workgroup: thread t ranks
+// request t % 128 against half t / 128 of the keys (broadcast LDS reads), the halves add up.
+constexpr int kPlanThreads = 2 * kBundleMaxBatch;
+__global__ void __launch_bounds__(kPlanThreads) decode_plan_kernel(const int64_t *pos, int B, int ctx, int2 *plan) {
+    __shared__ __attribute__((aligned(16))) int keys[kBundleMaxBatch];
+    __shared__ int part[kPlanThreads];
+    const int t = threadIdx.x, b = t % kBundleMaxBatch, half = t / kBundleMaxBatch;
+    int L = 0;
+    if (b < B) {
+        const int64_t pb = pos[b];
+        L = (pb >= 0 && pb < ctx) ? (int)pb + 1 : 0;
+    }
+    // ctx <= 2^20 keeps L << 7 below 2^31; b < 128 fits the low 7 bits
+    const int key = b < B ? (L << 7) | (kBundleMaxBatch - 1 - b) : -1;
+    if (half == 0) keys[b] = key;
+    __syncthreads();
+    int rank = 0;
+    constexpr int kHalf = kBundleMaxBatch / 2;
+#pragma unroll
+    for (int j = 0; j < kHalf / 4; ++j) {
+        const i32x4_t k4 = *(const i32x4_t *)&keys[half * kHalf + 4 * j];
+        rank += (k4.x > key) + (k4.y > key) + (k4.z > key) + (k4.w > key);
+    }
+    part[t] = rank;
+    __syncthreads();
+    if (half == 0 && b < B) plan[rank + part[t + kBundleMaxBatch]] = int2{b, L};
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1458,6 +1571,7 @@ static int decode_params(const q3t_decode_args *a, char *ws, DecodeParams &p) {
     p.qnw = nullptr;
     p.knw = nullptr;
     p.eps = a->norm_eps;
+    p.plan = grid == Q3T_GRID_BUNDLED ? a->plan : nullptr;  // only the bundled grid ranks requests
     if (a->q_norm_weight || a->k_norm_weight) {
         if (!fused || !(a->norm_eps >= 0.f)) return Q3T_EINVAL;
         if ((a->q_norm_weight && !aligned(a->q_norm_weight, 16)) ||
@@ -1555,4 +1669,13 @@ extern "C" int q3t_decode_attention(const q3t_decode_args *a, void *stream) {
     const int64_t need = q3t_decode_workspace_bytes(a);
     if (!a->workspace || a->workspace_bytes < need || !aligned(a->workspace, 16)) return Q3T_EWORKSPACE;
     return decode_launch(a, p, stream);
+}
+
+extern "C" int q3t_decode_plan(const int64_t *positions, int64_t batch, int64_t ctx, int32_t *plan, void *stream) {
+    if (batch < 0 || batch > kBundleMaxBatch || ctx < 1 || ctx > (1 << 20)) return Q3T_EINVAL;
+    if (batch == 0) return Q3T_OK;
+    if (!positions || !plan || !aligned(positions, 8) || !aligned(plan, 8)) return Q3T_EINVAL;
+    hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, (hipStream_t)stream, positions,
+                       (int)batch, (int)ctx, reinterpret_cast<int2 *>(plan));
+    return launch_status();
 }

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol(pkg):
 
 def test_status_strings_and_version(pkg):
     lib = pkg.library()
-    assert lib.q3t_abi_version() == 5
+    assert lib.q3t_abi_version() == 6
     assert lib.q3t_status_string(0) == b"success"
     assert lib.q3t_status_string(-1) == b"invalid argument"
     assert lib.q3t_status_string(-3) == b"workspace missing or too small"
@@ -81,6 +81,11 @@ def test_rejected_calls_return_negative_status_without_a_gpu(pkg):
     assert lib.q3t_decode_attention(args, None) == -2   # two query tokens: not on the bundled grid
     args.grid, args.query_len = 0, 1
     assert lib.q3t_decode_reset_workspace(None, 1 << 20, None) == -3
+    assert lib.q3t_decode_plan(None, 4, 1024, 16, None) == -1      # no positions
+    assert lib.q3t_decode_plan(16, 129, 1024, 16, None) == -1      # more requests than a plan ranks
+    assert lib.q3t_decode_plan(16, 4, 0, 16, None) == -1           # no arena rows
+    assert lib.q3t_decode_plan(16, 4, (1 << 20) + 1, 16, None) == -1
+    assert lib.q3t_decode_plan(None, 0, 1024, None, None) == 0     # an empty batch launches nothing
     # the allocation-free entry point refuses, before touching any device, a call whose split
     # states would not fit its fixed 8 MiB array (1024 requests x 8 heads x 16 chunks)
     big = pkg._lib.DecodeArgs()

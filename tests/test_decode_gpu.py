@@ -144,6 +144,59 @@ def test_bundled_grid_edges(pkg, device, group, batch, capacity, fused):
     idx = np.flatnonzero(valid.numpy())
     expected = oatt.decode_attention(query[idx], keys[idx], values[idx], contexts.numpy()[idx], D ** -0.5)
     assert_attention_close(got[idx], expected)
+    # the same launch from the step's plan: the same bundles, so the same bits
+    plan = pkg.decode_plan(positions, capacity)
+    if fused:
+        k2, v2 = torch.from_numpy(before_k.view(np.int16)).view(torch.bfloat16).to(device), \
+            torch.from_numpy(before_v.view(np.int16)).view(torch.bfloat16).to(device)
+        planned = pkg.decode_step(q, kn, vn, k2, v2, positions, cos, sin, grid="bundled", plan=plan)
+        assert np.array_equal(bits(k2), bits(k)) and np.array_equal(bits(v2), bits(v))
+    else:
+        planned = pkg.decode_attention(q, k, v, positions, grid="bundled", plan=plan)
+    assert torch.equal(planned, out)
+
+
+def _plan_expected(contexts, capacity):
+    lengths = np.where((contexts >= 0) & (contexts < capacity), contexts + 1, 0)
+    order = np.lexsort((np.arange(len(contexts)), -lengths))  # longest first, ties by index
+    return np.stack([order, lengths[order]], 1).astype(np.int32)
+
+
+@pytest.mark.parametrize("batch", [1, 6, 64, 100, 128])
+def test_decode_plan_ranks_longest_first(pkg, device, batch):
+    """The step's ranking against a stable numpy sort: ties (repeated lengths) by request
+    index, invalid positions (negative, at or past the capacity) ranked last with 0 keys."""
+    capacity = 1024
+    gen = torch.Generator().manual_seed(900 + batch)
+    contexts = torch.randint(-2, capacity + 2, (batch,), generator=gen)
+    contexts[: batch // 3] = contexts[0]  # ties
+    plan = pkg.decode_plan(contexts.to(device), capacity)
+    assert plan.shape == (batch, 2) and plan.dtype == torch.int32
+    np.testing.assert_array_equal(plan.cpu().numpy(), _plan_expected(contexts.numpy(), capacity))
+    with pytest.raises(ValueError):
+        pkg.decode_plan(torch.zeros(129, dtype=torch.int64, device=device), capacity)
+
+
+def test_decode_plan_of_other_positions_stays_in_bounds(pkg, device):
+    """A plan is only valid for the positions it was made from.  A stale or malformed one
+    (request indices outside the batch, lengths past the arena) gives other outputs but
+    touches nothing outside the arguments: entries naming no request are skipped, lengths are
+    clamped to the arena, and the output rows of requests it does not name stay as they were."""
+    contexts, k, v, q, kn, vn = _config2(device, seed=13)
+    positions = contexts.to(device)
+    cos, sin = pkg.rope_tables(positions, D)
+    bad = pkg.decode_plan(positions, 1024).clone()
+    bad[::3, 0] = 1000      # no such request
+    bad[1::3, 1] = 5000     # more keys than the arena has
+    out = torch.full((64, 1, HQ, D), 7.0, device=device, dtype=torch.bfloat16)
+    pkg.decode_attention(q, k, v, positions, grid="bundled", plan=bad, out=out)
+    torch.cuda.synchronize()
+    named = set(bad[:, 0].cpu().tolist())
+    for b in range(64):
+        if b not in named:
+            assert torch.all(out[b] == 7.0)
+    with pytest.raises(ValueError):
+        pkg.decode_attention(q, k, v, positions, grid="bundled", plan=bad[:10])
 
 
 def test_bundled_grid_is_deterministic_and_refuses_what_it_cannot_run(pkg, device):
