@@ -884,7 +884,9 @@ struct Slots4 {
     }
 };
 
-template <int G, bool FUSED, bool STREAM>
+// NORM: the fused q/k RMSNorm is compiled in (a separate instance: its code, even unexecuted,
+// cost the talker step 1.8 us per launch in the instance without norms).
+template <int G, bool FUSED, bool STREAM, bool NORM>
 __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(DecodeParams p) {
     static_assert(G >= 1 && G <= 4, "query rows are the first G of 16 MFMA columns, four LDS rows");
     __shared__ __attribute__((aligned(16))) BundleLds<G> s;
@@ -897,7 +899,7 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(DecodeParams p
     // before any ring load is issued: a wait the compiler placed at their first use would also
     // wait for the ring's loads, which it does not count
     U4 qw = {0u, 0u, 0u, 0u}, kw = {0u, 0u, 0u, 0u};
-    if constexpr (FUSED) {
+    if constexpr (FUSED && NORM) {
         if (p.qnw) qw = load16(p.qnw + c * 16);
         if (p.knw) kw = load16(p.knw + c * 16);
     }
@@ -1084,6 +1086,38 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(DecodeParams p
     issue_next();
     if (issued < total) issue_next();
 
+    {
+        // the rows landed before the stages (which stay in flight)
+        if (issued == 1) wait_loads<kStageLoads>();
+        else wait_loads<2 * kStageLoads>();
+        if constexpr (FUSED) {
+            // each request's rows in the wave that loaded them, while the first stages are in
+            // flight: lane group r < G holds query row r and lane group G the step's key (a
+            // second pass for G = 4), lane c chunk c; normalised, rotated and written back
+#pragma unroll
+            for (int k = 0; k < kBundleMaxSeg; ++k) {
+                if (k >= nseg || tb_l.get(k) == 0 || wave != k % kWaves) continue;
+                const int Lk = tb_l.get(k);
+                const uint32_t hk = head_of(k);
+                const U4 cv = lds_read16(hk + 4 * kRowBytes + c * 16), sv = lds_read16(hk + 5 * kRowBytes + c * 16);
+                auto rotate = [&](int row, bool is_key) {
+                    U4 x = lds_read16(hk + row * kRowBytes + c * 16);
+                    if constexpr (NORM) {
+                        if (is_key ? p.knw != nullptr : p.qnw != nullptr) x = rms_norm8<16>(x, is_key ? kw : qw, p.eps, 128);
+                    }
+                    return rope_half8(x, xor8_u4(x), cv, sv, c < 8);
+                };
+                if constexpr (G < 4) {
+                    if (g <= G) lds_write16(hk + (g < G ? g : 6) * kRowBytes + c * 16, rotate(g < G ? g : 6, g == G));
+                } else {
+                    lds_write16(hk + g * kRowBytes + c * 16, rotate(g, false));
+                    if (g == 0) lds_write16(hk + 6 * kRowBytes + c * 16, rotate(6, true));
+                }
+            }
+        }
+        lds_barrier();  // every request's rows, rotated, visible to every wave
+    }
+
     // per-lane LDS offsets within a wave's stage: K rows as the A operand of S^T (row c, dims
     // 32 kk + 8 g ...), V rows for the transposing read (row 4g + c/4, 4 dims)
     uint32_t ka[4], va[8];
@@ -1107,35 +1141,6 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(DecodeParams p
         // the next stage, into the slot scored last (the first two went out before the loop)
         if (issued < total && issued <= t + 1) issue_next();
         const int ahead = issued - 1 - t;  // stages issued after this one: 0 or 1
-        if (t == 0) {
-            // the rows landed before the stages (which stay in flight)
-            if (issued == 1) wait_loads<kStageLoads>();
-            else wait_loads<2 * kStageLoads>();
-            if constexpr (FUSED) {
-                // each request's rows in the wave that loaded them, while the first stages are in
-                // flight: lane group r < G holds query row r and lane group G the step's key (a
-                // second pass for G = 4), lane c chunk c; normalised, rotated and written back
-#pragma unroll
-                for (int k = 0; k < kBundleMaxSeg; ++k) {
-                    if (k >= nseg || tb_l.get(k) == 0 || wave != k % kWaves) continue;
-                    const int Lk = tb_l.get(k);
-                    const uint32_t hk = head_of(k);
-                    const U4 cv = lds_read16(hk + 4 * kRowBytes + c * 16), sv = lds_read16(hk + 5 * kRowBytes + c * 16);
-                    auto rotate = [&](int row, bool is_key) {
-                        U4 x = lds_read16(hk + row * kRowBytes + c * 16);
-                        if (is_key ? p.knw != nullptr : p.qnw != nullptr) x = rms_norm8<16>(x, is_key ? kw : qw, p.eps, 128);
-                        return rope_half8(x, xor8_u4(x), cv, sv, c < 8);
-                    };
-                    if constexpr (G < 4) {
-                        if (g <= G) lds_write16(hk + (g < G ? g : 6) * kRowBytes + c * 16, rotate(g < G ? g : 6, g == G));
-                    } else {
-                        lds_write16(hk + g * kRowBytes + c * 16, rotate(g, false));
-                        if (g == 0) lds_write16(hk + 6 * kRowBytes + c * 16, rotate(6, true));
-                    }
-                }
-            }
-            lds_barrier();  // every request's rows, rotated, visible to every wave
-        }
         if (cj == 0) {
             // a new request: its rows as B operands, columns c >= G zero
             const U4 zero = {0u, 0u, 0u, 0u};
@@ -1441,10 +1446,16 @@ static void launch_decode(const DecodeParams &p, hipStream_t s) {
     if constexpr (sizeof(T) == 2 && D == 128 && SQ == 1 && !M && G <= 4) {
         if (p.bundles > 0) {
             const dim3 grid((uint32_t)p.bundles * p.Hkv);
-            if (p.stream)
-                hipLaunchKernelGGL((decode_bundled_kernel<G, F, true>), grid, dim3(kThreads), 0, s, p);
-            else
-                hipLaunchKernelGGL((decode_bundled_kernel<G, F, false>), grid, dim3(kThreads), 0, s, p);
+            if (F && (p.qnw || p.knw)) {
+                if constexpr (F) {
+                    if (p.stream) hipLaunchKernelGGL((decode_bundled_kernel<G, F, true, true>), grid, dim3(kThreads), 0, s, p);
+                    else hipLaunchKernelGGL((decode_bundled_kernel<G, F, false, true>), grid, dim3(kThreads), 0, s, p);
+                }
+            } else if (p.stream) {
+                hipLaunchKernelGGL((decode_bundled_kernel<G, F, true, false>), grid, dim3(kThreads), 0, s, p);
+            } else {
+                hipLaunchKernelGGL((decode_bundled_kernel<G, F, false, false>), grid, dim3(kThreads), 0, s, p);
+            }
             return;
         }
     }
