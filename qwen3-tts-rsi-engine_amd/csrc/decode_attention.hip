@@ -271,8 +271,11 @@ constexpr int decode_waves_per_eu(int es, int rows, bool mask) {
 //              range's merged state in wave 0: for output t = lane + 64 i (query row
 //              t / D, dim t % D) the unnormalised accumulator A[i], the weight sum Ls[i]
 //              and the running maximum Mx[i] in scaled log2 units.
-template <typename T, int D, int G, int SQ, bool FUSED, bool MASK, bool STREAM, bool PIPE>
+template <typename T, int D, int G, int SQ, int FUSE, bool MASK, bool STREAM, bool PIPE>
 struct PairWork {
+    // FUSE: 0 attention only, 1 the fused step, 2 the fused step with its q/k norms (a separate
+    // instance: the norm code, even unexecuted, slowed the fused bundled kernel by 1.8 us)
+    static constexpr bool FUSED = FUSE > 0, NORM = FUSE > 1;
     static constexpr int R = G * SQ;
     using S = DecodeShape<T, D>;
     static constexpr int LPK = S::LPK, CW = S::CW, RPW = S::RPW, RPP = S::RPP, P = S::P, ES = S::ES;
@@ -375,7 +378,7 @@ struct PairWork {
 #pragma unroll
         for (int r = 0; r < R; ++r) q[r] = qr[r];
         if constexpr (FUSED) {
-            if (p.qnw) {
+            if (NORM && p.qnw) {
                 const U4 w = load16(p.qnw + cl * 16);
 #pragma unroll
                 for (int r = 0; r < R; ++r) q[r] = rms_norm8<LPK>(q[r], w, p.eps, D);
@@ -388,7 +391,7 @@ struct PairWork {
                 const U4 ct = SQ == 1 || grp == 0 ? cv[0] : cv[SQ - 1];
                 const U4 st = SQ == 1 || grp == 0 ? sv[0] : sv[SQ - 1];
                 U4 kx = nk;
-                if (p.knw) kx = rms_norm8<LPK>(nk, load16(p.knw + cl * 16), p.eps, D);
+                if (NORM && p.knw) kx = rms_norm8<LPK>(nk, load16(p.knw + cl * 16), p.eps, D);
                 const U4 kn = rope_half8(kx, xor8_u4(kx), ct, st, cl < 8);
                 const int row = L - SQ + grp;
                 buffer_store16(krs, (uint32_t)(row * kst) + cl * 16, kn);
@@ -649,11 +652,12 @@ Q3T_DEVICE void finish_split(const DecodeParams &p, int b, int h, int n, int k, 
 // ---- chunked grid: one workgroup per (request, chunk, KV head) ------------------------
 // For short contexts (the code predictor's 16-row caches): every pair's rows are requested
 // together with its position, so a workgroup's whole life is two memory round trips.
-template <typename T, int D, int G, int SQ, bool FUSED, bool MASK, bool STREAM>
+template <typename T, int D, int G, int SQ, int FUSE, bool MASK, bool STREAM>
 __global__ void __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(decode_waves_per_eu(sizeof(T), G * SQ, MASK))))
 decode_chunks_kernel(DecodeParams p) {
-    using Work = PairWork<T, D, G, SQ, FUSED, MASK, STREAM, false>;
+    using Work = PairWork<T, D, G, SQ, FUSE, MASK, STREAM, false>;
+    constexpr bool FUSED = Work::FUSED;
     constexpr int OPL = Work::OPL, R = Work::R;
     __shared__ typename Work::Lds lds;
     __shared__ typename Work::NewRows snew;
@@ -710,10 +714,11 @@ decode_chunks_kernel(DecodeParams p) {
 constexpr bool kBalancedPipe = true;
 constexpr int balanced_waves_per_eu(int rows) { return rows <= 2 ? 2 : 1; }
 
-template <typename T, int D, int G, int SQ, bool FUSED, bool MASK, bool STREAM>
+template <typename T, int D, int G, int SQ, int FUSE, bool MASK, bool STREAM>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(balanced_waves_per_eu(G * SQ))))
 decode_balanced_kernel(DecodeParams p) {
-    using Work = PairWork<T, D, G, SQ, FUSED, MASK, STREAM, kBalancedPipe>;
+    using Work = PairWork<T, D, G, SQ, FUSE, MASK, STREAM, kBalancedPipe>;
+    constexpr bool FUSED = Work::FUSED;
     constexpr int OPL = Work::OPL, R = Work::R;
     constexpr int PER = kMaxBatch / kThreads;  // requests per thread at most
     __shared__ typename Work::Lds lds[2];      // alternate segments: wave 0 may still read one
@@ -1439,10 +1444,28 @@ extern "C" int64_t q3t_decode_workspace_bytes(const q3t_decode_args *a) {
     return counters_bytes() + partial_floats(a) * 4;
 }
 
-template <typename T, int D, int G, int SQ, bool F, bool M>
-static void launch_decode(const DecodeParams &p, hipStream_t s) {
+// The chunked and balanced grids (FUSE as in PairWork).
+template <typename T, int D, int G, int SQ, int FUSE, bool M>
+static void launch_split(const DecodeParams &p, hipStream_t s) {
     // streamed instances only for the talker-shaped single-query launches
     constexpr bool can_stream = sizeof(T) == 2 && D == 128 && SQ == 1;
+    if (p.splits > 0) {
+        const dim3 grid((uint32_t)p.splits * p.Hkv);
+        if (can_stream && p.stream)
+            hipLaunchKernelGGL((decode_balanced_kernel<T, D, G, SQ, FUSE, M, can_stream>), grid, dim3(kThreads), 0, s, p);
+        else
+            hipLaunchKernelGGL((decode_balanced_kernel<T, D, G, SQ, FUSE, M, false>), grid, dim3(kThreads), 0, s, p);
+        return;
+    }
+    const dim3 grid((uint32_t)p.B * p.Hkv * p.nchunks);
+    if (can_stream && p.stream)
+        hipLaunchKernelGGL((decode_chunks_kernel<T, D, G, SQ, FUSE, M, can_stream>), grid, dim3(kThreads), 0, s, p);
+    else
+        hipLaunchKernelGGL((decode_chunks_kernel<T, D, G, SQ, FUSE, M, false>), grid, dim3(kThreads), 0, s, p);
+}
+
+template <typename T, int D, int G, int SQ, bool F, bool M>
+static void launch_decode(const DecodeParams &p, hipStream_t s) {
     if constexpr (sizeof(T) == 2 && D == 128 && SQ == 1 && !M && G <= 4) {
         if (p.bundles > 0) {
             const dim3 grid((uint32_t)p.bundles * p.Hkv);
@@ -1459,19 +1482,13 @@ static void launch_decode(const DecodeParams &p, hipStream_t s) {
             return;
         }
     }
-    if (p.splits > 0) {
-        const dim3 grid((uint32_t)p.splits * p.Hkv);
-        if (can_stream && p.stream)
-            hipLaunchKernelGGL((decode_balanced_kernel<T, D, G, SQ, F, M, can_stream>), grid, dim3(kThreads), 0, s, p);
-        else
-            hipLaunchKernelGGL((decode_balanced_kernel<T, D, G, SQ, F, M, false>), grid, dim3(kThreads), 0, s, p);
-        return;
+    if constexpr (F) {
+        if (p.qnw || p.knw) {
+            launch_split<T, D, G, SQ, 2, M>(p, s);
+            return;
+        }
     }
-    const dim3 grid((uint32_t)p.B * p.Hkv * p.nchunks);
-    if (can_stream && p.stream)
-        hipLaunchKernelGGL((decode_chunks_kernel<T, D, G, SQ, F, M, can_stream>), grid, dim3(kThreads), 0, s, p);
-    else
-        hipLaunchKernelGGL((decode_chunks_kernel<T, D, G, SQ, F, M, false>), grid, dim3(kThreads), 0, s, p);
+    launch_split<T, D, G, SQ, F ? 1 : 0, M>(p, s);
 }
 
 template <typename T, int D, int G>
