@@ -160,7 +160,8 @@ class PackedAttention(torch.nn.Module):
         return cos, sin
 
     def _fused_target(self, cache, attention_mask, batch, length, query):
-        """(keys, values, positions, mask) of a step the fused launch can take, else None.
+        """(keys, values, positions, mask, plan) of a step the fused launch can take, else None
+        (plan: the slot cache's ranking of the step's requests, SlotCache.prepare).
 
         The mask the layer is given is applied in the launch (the reference's operator applies
         it, npu_attention.py:16-25), except the predictor's first-step 2x2 causal mask, which
@@ -176,19 +177,19 @@ class PackedAttention(torch.nn.Module):
                 keys, values = cache.keys[layer], cache.values[layer]
                 if (keys.is_contiguous() and values.is_contiguous() and keys.shape[0] == batch
                         and keys.shape[2] >= 2):
-                    return keys, values, cache.positions_at(batch, 1, query.device), None
+                    return keys, values, cache.positions_at(batch, 1, query.device), None, None
             return None
         if attention_mask is not None and not isinstance(attention_mask, torch.Tensor):
             return None
         if isinstance(cache, SlotCache):
             keys, values = cache.arena.keys[layer], cache.arena.values[layer]
             if keys.is_contiguous() and values.is_contiguous():
-                return keys, values, cache.positions, attention_mask
+                return keys, values, cache.positions, attention_mask, cache.plan
         elif isinstance(cache, PredictorCache) and cache.step >= 1:
             keys, values = cache.keys[layer], cache.values[layer]
             if (keys.is_contiguous() and values.is_contiguous() and keys.shape[0] == batch
                     and cache.step + 1 < keys.shape[2]):
-                return keys, values, cache.positions_at(batch, cache.step + 1, query.device), attention_mask
+                return keys, values, cache.positions_at(batch, cache.step + 1, query.device), attention_mask, None
         return None
 
     def _prefill(self, query, key, value, cos, sin, cache, batch, length):
@@ -229,15 +230,17 @@ class PackedAttention(torch.nn.Module):
 
         fused = self._fused_target(past_key_values, attention_mask, batch, length, query)
         if fused is not None:
-            keys, values, positions, mask = fused
+            keys, values, positions, mask, plan = fused
+            if plan is not None and plan.shape[0] != batch:
+                plan = None
             if self._norms is not None and self._norms[0].device == query.device:
                 q_weight, k_weight, eps = self._norms
                 output = decode_step(query, key, value, keys, values, positions, cos, sin,
                                      scale=reference.scaling, q_norm_weight=q_weight,
-                                     k_norm_weight=k_weight, norm_eps=eps, mask=mask)
+                                     k_norm_weight=k_weight, norm_eps=eps, mask=mask, plan=plan)
             else:
                 output = decode_step(reference.q_norm(query), reference.k_norm(key), value, keys, values,
-                                     positions, cos, sin, scale=reference.scaling, mask=mask)
+                                     positions, cos, sin, scale=reference.scaling, mask=mask, plan=plan)
             return reference.o_proj(output.reshape(*shape, -1)), None
 
         query = reference.q_norm(query)

@@ -175,3 +175,41 @@ def test_mask_is_built_only_for_unwrapped_layers(pkg, device):
     allowed = torch.arange(48, device=device)[None, :] <= graph.positions[:, None]
     assert torch.equal(mask[:, 0, 0] == 0, allowed)
     assert bool((mask[:, 0, 0][~allowed] == torch.finfo(torch.bfloat16).min).all())
+
+
+def test_talker_step_on_the_bundled_grid_reads_the_step_plan(pkg, device):
+    """At the talker's shape (64 slots of a 1024-row arena, 8 KV heads of 128: the bundled
+    grid) SlotCache.prepare ranks the step's requests once (decode_plan) and every layer's
+    launch reads that ranking: replays equal an eager twin whose cache holds no plan (each
+    launch ranks the requests itself), output and arena bit-identical, and the plan equals a
+    stable sort by length."""
+    slots, capacity, batch = 64, 1024, 64
+    model = _model(pkg, device, layers=2)
+    arena = _arena(pkg, model, slots, capacity, 24)
+    twin_arena = pkg.SlotArena(model, slots, capacity, packed_kv=True)
+    twin_arena.packed.copy_(arena.packed)
+    assert pkg.decode_grid_for(batch, 1, 16, 8, 128, capacity) == 'bundled'
+    graph = pkg.SlotGraph(arena, batch)
+    graph.capture()
+    twin = pkg.SlotGraph(twin_arena, batch)
+    twin.cache.prepare = lambda: None                        # no plan: in-launch ranking
+    gen = torch.Generator().manual_seed(25)
+    for step, count in enumerate([64, 40]):
+        positions = torch.zeros(batch, dtype=torch.long)
+        positions[:count] = torch.randint(0, capacity, (count,), generator=gen)
+        inputs = torch.randn(batch, 1, model.config.hidden_size, generator=gen).bfloat16().to(device)
+        rotary = positions.view(1, batch, 1).expand(3, batch, 1).to(device)
+        out = graph.run(inputs, positions.to(device), rotary)
+        with torch.inference_mode():
+            twin.inputs.copy_(inputs)
+            twin.positions.copy_(positions.to(device))
+            twin.rotary.copy_(rotary)
+            expected = twin.compute()
+        torch.cuda.synchronize()
+        assert twin.cache.plan is None and graph.cache.plan is not None
+        lengths = positions.numpy() + 1
+        order = np.lexsort((np.arange(batch), -lengths))
+        np.testing.assert_array_equal(graph.cache.plan.cpu().numpy(), np.stack([order, lengths[order]], 1))
+        assert np.array_equal(bits(out), bits(expected)), f"step {step}"
+        assert np.array_equal(bits(arena.packed), bits(twin_arena.packed)), f"step {step}"
+    graph.close()
