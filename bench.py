@@ -3,9 +3,10 @@
 Workload (the talker decode-attention step): 64 concurrent requests with context lengths
 c_b = torch.randint(64, 1025, (64,)) under seed 0 (sum 32,718), a packed bf16 KV arena
 (2*28 planes, 64 slots, 8 KV heads, capacity 1024, head_dim 128), 16 query heads, RoPE
-theta 1e6.  One step = 28 layers; each layer is one fused HIP launch doing RoPE of q and of
-the new key, the paired K/V write at position c_b and ragged GQA decode attention over
-c_b + 1 keys.  The 28 launches of a step are captured once into a HIP graph and replayed.
+theta 1e6.  One step = the ranking of the 64 requests by length (one small launch, read by
+every layer) and 28 layers; each layer is one fused HIP launch doing RoPE of q and of the new
+key, the paired K/V write at position c_b and ragged GQA decode attention over c_b + 1 keys.
+The 29 launches of a step are captured once into a HIP graph and replayed.
 Inputs are synthetic (seeded random, resident in HBM before timing).
 
 Prints one JSON line: tokens/s (64 tokens per step), the dominant kernel's roofline
@@ -407,7 +408,7 @@ def trace_detail(pkg, device, iterations=200, slots=128):
             "arena_ops_us_total": arena_us}
 
 
-KERNELS = {"bundled": "decode_bundled_kernel<G2,fused,streamed>",
+KERNELS = {"bundled": "decode_bundled_kernel<G2,fused,streamed,no norm>",
            "balanced": "decode_balanced_kernel<bf16,128,G2,SQ1,fused,streamed>",
            "chunked": "decode_chunks_kernel<bf16,128,G2,SQ1,fused,streamed>"}
 
