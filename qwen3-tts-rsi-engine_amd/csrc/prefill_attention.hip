@@ -437,18 +437,25 @@ prefill_attention_kernel(PrefillParams p) {
             float mx = x[0];
 #pragma unroll
             for (int e = 1; e < 8; ++e) mx = __builtin_amdgcn_fmed3f(mx, x[e], __builtin_inff());
-            mx = __builtin_amdgcn_fmed3f(mx, xor16(mx), __builtin_inff());
-            mx = __builtin_amdgcn_fmed3f(mx, xor32(mx), __builtin_inff());
-            const float mt = MB ? fmaxf(mx, kEmptyP) : mx * sl;  // a fully masked step keeps m finite
-            if (first) {
-                m[j] = mt;
-            } else if (__builtin_amdgcn_ballot_w64(mt > m[j] + kRescaleLog2) != 0) {
-                const float mn = fmaxf(m[j], mt);
-                const float alpha = fexp2(m[j] - mn);
-                m[j] = mn;
-                l[j] *= alpha;
+            // the step maximum of a query is the largest of its four lanes' maxima (scaling is
+            // monotonic, so it commutes with the maximum): some query exceeds its running maximum
+            // by more than kRescaleLog2 exactly when some lane's own maximum does, and the
+            // maximum across lanes is needed only to start and to rescale
+            float mt = MB ? mx : mx * sl;
+            if (first || __builtin_amdgcn_ballot_w64(mt > m[j] + kRescaleLog2) != 0) {
+                mt = __builtin_amdgcn_fmed3f(mt, xor16(mt), __builtin_inff());
+                mt = __builtin_amdgcn_fmed3f(mt, xor32(mt), __builtin_inff());
+                if constexpr (MB > 0) mt = fmaxf(mt, kEmptyP);  // a fully masked step keeps m finite
+                if (first) {
+                    m[j] = mt;
+                } else {
+                    const float mn = fmaxf(m[j], mt);
+                    const float alpha = fexp2(m[j] - mn);
+                    m[j] = mn;
+                    l[j] *= alpha;
 #pragma unroll
-                for (int db = 0; db < DB; ++db) acc[j][db] *= alpha;
+                    for (int db = 0; db < DB; ++db) acc[j][db] *= alpha;
+                }
             }
             float pv[8];
 #pragma unroll
