@@ -52,6 +52,21 @@ def attention_bytes(contexts: torch.Tensor) -> int:
     return (int(contexts.sum()) + BATCH) * HKV * D * 2 * 2 + BATCH * HQ * D * 2 * 2 + BATCH * 8
 
 
+def calibration_copy(pkg, device, nbytes, stream):
+    """The plain copy kernel over ``nbytes`` (three launches), so that rocprofv3's
+    FETCH_SIZE / WRITE_SIZE of a run can be scaled by what they read for a copy of known size."""
+    if nbytes <= 0:
+        return
+    n = nbytes // 16 * 16
+    src = torch.empty(n, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        status = pkg.library().q3t_copy_bytes(dst.data_ptr(), src.data_ptr(), n, stream.cuda_stream)
+        if status != 0:
+            raise RuntimeError("calibration copy failed")
+    torch.cuda.synchronize()
+
+
 def prefill_detail(pkg, device, reps=20):
     """The prefill workload: 16 prompts, lengths randint(32, 513, (16,)) under seed 0
     (sum 4790), 28 layers of RoPE + arena write + varlen causal GQA in one graph.
@@ -451,6 +466,7 @@ def main():
     torch.cuda.set_device(device)
     if args.prefill_only:
         print(json.dumps({"prefill": prefill_detail(pkg, device)}), flush=True)
+        calibration_copy(pkg, device, args.calibrate_bytes, torch.cuda.current_stream(device))
         return
     gen = torch.Generator().manual_seed(0)
     contexts = torch.randint(64, 1025, (BATCH,), generator=gen)
@@ -525,15 +541,7 @@ def main():
     torch.cuda.synchronize()
     attn_us = start.elapsed_time(stop) * 1e3 / (reps * LAYERS)
 
-    if args.calibrate_bytes > 0:
-        n = args.calibrate_bytes // 16 * 16
-        src = torch.empty(n, dtype=torch.uint8, device=device)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            status = pkg.library().q3t_copy_bytes(dst.data_ptr(), src.data_ptr(), n, stream.cuda_stream)
-            if status != 0:
-                raise RuntimeError("calibration copy failed")
-        torch.cuda.synchronize()
+    calibration_copy(pkg, device, args.calibrate_bytes, stream)
 
     extra = {}
     if not args.decode_only:
