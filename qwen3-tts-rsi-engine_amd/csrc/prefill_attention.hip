@@ -242,12 +242,15 @@ prefill_attention_kernel(PrefillParams p) {
     // the requests with a block there (ballot) and the item's request is picked by rank
     // (mbcnt), all wave-uniform, with no memory access beyond the row offsets.
     int b, qb, t0, n, kn;
+    int64_t slot;
     if (p.B <= 64) {
         int start = 0, rows = 0, klen = 0;
+        int64_t slot_l = 0;  // the request's arena slot, loaded with its rows (no later round trip)
         if (lane < p.B) {
             start = p.cu[lane];
             rows = (start < 0 || start >= p.T) ? 0 : (int)min((int64_t)(p.cu[lane + 1] - start), p.T - start);
             klen = p.kvl ? p.kvl[lane] : rows;
+            slot_l = p.slots ? p.slots[lane] : lane;
         }
         const int blocks = rows > 0 ? (rows + kQBlock - 1) / kQBlock : 0;
         int remaining = rest;
@@ -270,6 +273,8 @@ prefill_attention_kernel(PrefillParams p) {
         t0 = __builtin_amdgcn_readlane(start, b);
         n = __builtin_amdgcn_readlane(rows, b);
         kn = __builtin_amdgcn_readlane(klen, b);
+        slot = ((int64_t)__builtin_amdgcn_readlane((int)(slot_l >> 32), b) << 32) |
+               (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)slot_l, b);
     } else {
         b = rest % p.B;
         qb = p.nqb - 1 - rest / p.B;  // the longest blocks are dispatched first
@@ -277,6 +282,7 @@ prefill_attention_kernel(PrefillParams p) {
         if (t0 < 0 || t0 >= p.T) return;
         n = (int)min((int64_t)(p.cu[b + 1] - t0), p.T - t0);  // rows past the packed tokens do not exist
         kn = p.kvl ? p.kvl[b] : n;
+        slot = p.slots ? p.slots[b] : b;
     }
     const int q0 = qb * kQBlock;
     if (q0 >= n) return;
@@ -284,7 +290,6 @@ prefill_attention_kernel(PrefillParams p) {
     // Causal: up to the block's last query and the request's key count; masked: every key.
     const int kv_end = MB ? (int)p.cap : (int)min((int64_t)min(min(n, kn), q0 + kQBlock), p.cap);
     const int ntiles = kv_end > 0 ? (kv_end + kTile - 1) / kTile : 0;
-    const int64_t slot = p.slots ? p.slots[b] : b;
     const int wq0 = q0 + 16 * wave;              // first query of this wave
     // keys [0, wave_end) can be visible to the wave; steps reaching past mask_from need the
     // per-key rule (the diagonal or the end of the keys)
