@@ -18,10 +18,15 @@ LIBRARY = PACKAGE_DIR / "libq3t_amd.so"
 ARCH = "gfx950"
 
 # Packed-fp32 VALU forms are kept out of the generated code (hipcc warns that the host
-# pass does not know the feature; that warning is harmless).
+# pass does not know the feature; that warning is harmless).  Kernels' leading scalar and
+# pointer arguments (up to six dwords) are preloaded into scalar registers at wave launch, so
+# a kernel can issue its first dependent load without waiting for its argument block (the
+# bundled decode passes its plan pointer and sizes that way; arguments passed as a structure
+# are not preloaded).
 HIP_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-kernarg-preload-count=6",
     "-Wno-unused-command-line-argument",
 ]
 

@@ -892,13 +892,42 @@ struct Slots4 {
 // NORM: the fused q/k RMSNorm is compiled in (a separate instance: its code, even unexecuted,
 // cost the talker step 1.8 us per launch in the instance without norms).
 template <int G, bool FUSED, bool STREAM, bool NORM>
-__global__ void __launch_bounds__(kThreads) decode_bundled_kernel(DecodeParams p) {
+__global__ void __launch_bounds__(kThreads) decode_bundled_kernel(const int32_t *plan, int nb, int hkv, int bundles, DecodeParams p) {
     static_assert(G >= 1 && G <= 4, "query rows are the first G of 16 MFMA columns, four LDS rows");
     __shared__ __attribute__((aligned(16))) BundleLds<G> s;
-    prefetch_kernargs<sizeof(DecodeParams)>();
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS bases stay scalar
-    const int h = blockIdx.x % p.Hkv, m = blockIdx.x / p.Hkv, M = p.bundles;
+    const int h = blockIdx.x % hkv, m = blockIdx.x / hkv, M = bundles;
+    // The plan entries of this bundle and every line of the argument block in one scalar round
+    // trip: the plan pointer and the sizes its addresses need are the leading kernel arguments,
+    // which the hardware preloads into scalar registers.
+    auto bundle_rank = [&](int i) { return (i >> 1) * 2 * M + ((i & 1) ? 2 * M - 1 - m : m); };
+    uint64_t e[kBundleMaxSeg] = {0, 0, 0, 0};
+    if (plan) {
+        const uint64_t base = reinterpret_cast<uint64_t>(plan);
+        uint64_t a[kBundleMaxSeg];
+#pragma unroll
+        for (int i = 0; i < kBundleMaxSeg; ++i)
+            a[i] = base + 8 * (uint64_t)(bundle_rank(i) < nb ? bundle_rank(i) : 0);
+        constexpr int BYTES = 32 + (int)sizeof(DecodeParams);
+        static_assert(BYTES <= 8 * 64, "eight 64-byte lines at most");
+        const uint64_t ka = reinterpret_cast<uint64_t>(__builtin_amdgcn_kernarg_segment_ptr());
+        uint32_t d0, d1, d2, d3, d4, d5, d6, d7;
+        asm volatile("s_load_dwordx2 %0, %12, 0x0\n\ts_load_dwordx2 %1, %13, 0x0\n\t"
+                     "s_load_dwordx2 %2, %14, 0x0\n\ts_load_dwordx2 %3, %15, 0x0\n\t"
+                     "s_load_dword %4, %16, 0x0\n\ts_load_dword %5, %16, 0x40\n\t"
+                     "s_load_dword %6, %16, 0x80\n\ts_load_dword %7, %16, 0xc0\n\t"
+                     "s_load_dword %8, %16, %17\n\ts_load_dword %9, %16, %18\n\t"
+                     "s_load_dword %10, %16, %19\n\ts_load_dword %11, %16, %20\n\t"
+                     "s_waitcnt lgkmcnt(0)"
+                     : "=&s"(e[0]), "=&s"(e[1]), "=&s"(e[2]), "=&s"(e[3]), "=&s"(d0), "=&s"(d1), "=&s"(d2),
+                       "=&s"(d3), "=&s"(d4), "=&s"(d5), "=&s"(d6), "=&s"(d7)
+                     : "s"(a[0]), "s"(a[1]), "s"(a[2]), "s"(a[3]), "s"(ka), "n"(BYTES > 0x100 ? 0x100 : 0),
+                       "n"(BYTES > 0x140 ? 0x140 : 0), "n"(BYTES > 0x180 ? 0x180 : 0), "n"(BYTES > 0x1c0 ? 0x1c0 : 0)
+                     : "memory");
+    } else {
+        prefetch_kernargs<32 + sizeof(DecodeParams)>();
+    }
 
     // weights of the fused norms (chunk c of the row), loaded with the positions and waited for
     // before any ring load is issued: a wait the compiler placed at their first use would also
@@ -914,7 +943,6 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(DecodeParams p
     Slots4<int> tb_b = {-1, -1, -1, -1}, tb_l = {0, 0, 0, 0};
     Slots4<int64_t> tb_k = {0, 0, 0, 0}, tb_v = {0, 0, 0, 0};
     int nseg = 0;
-    auto bundle_rank = [&](int i) { return (i >> 1) * 2 * M + ((i & 1) ? 2 * M - 1 - m : m); };
     auto set_slot = [&](int i, int b, int L) {
         const int64_t o = p.offs && b >= 0 ? p.offs[b] : 0;
         tb_b.set(i, b);
@@ -923,21 +951,11 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(DecodeParams p
         tb_v.set(i, (p.offs ? o : (int64_t)b * p.v_sb) + h * p.v_sh);
         nseg = i + 1;
     };
-    if (p.plan) {
+    if (plan) {
         // a ranking made once for the step's positions (q3t_decode_plan): (b, L) pairs, longest
-        // first.  One wave-uniform load round trip and no ranking here; entries that do not
-        // name a request of this batch attend nothing and write nothing.
-        // The four entries come in one scalar round trip (ranks past the batch read entry 0 and
-        // are ignored); written out, the compiler serialised them as vector loads.
-        const uint64_t base = reinterpret_cast<uint64_t>(p.plan);
-        uint64_t a[kBundleMaxSeg], e[kBundleMaxSeg];
-#pragma unroll
-        for (int i = 0; i < kBundleMaxSeg; ++i)
-            a[i] = base + 8 * (uint64_t)(bundle_rank(i) < p.B ? bundle_rank(i) : 0);
-        asm volatile("s_load_dwordx2 %0, %4, 0x0\n\ts_load_dwordx2 %1, %5, 0x0\n\t"
-                     "s_load_dwordx2 %2, %6, 0x0\n\ts_load_dwordx2 %3, %7, 0x0\n\ts_waitcnt lgkmcnt(0)"
-                     : "=&s"(e[0]), "=&s"(e[1]), "=&s"(e[2]), "=&s"(e[3])
-                     : "s"(a[0]), "s"(a[1]), "s"(a[2]), "s"(a[3]) : "memory");
+        // first, loaded above; no ranking here.  Entries that do not name a request of this
+        // batch attend nothing and write nothing (ranks past the batch read entry 0 and are
+        // ignored).
 #pragma unroll
         for (int i = 0; i < kBundleMaxSeg; ++i) {
             if (bundle_rank(i) >= p.B) continue;
@@ -1471,13 +1489,13 @@ static void launch_decode(const DecodeParams &p, hipStream_t s) {
             const dim3 grid((uint32_t)p.bundles * p.Hkv);
             if (F && (p.qnw || p.knw)) {
                 if constexpr (F) {
-                    if (p.stream) hipLaunchKernelGGL((decode_bundled_kernel<G, F, true, true>), grid, dim3(kThreads), 0, s, p);
-                    else hipLaunchKernelGGL((decode_bundled_kernel<G, F, false, true>), grid, dim3(kThreads), 0, s, p);
+                    if (p.stream) hipLaunchKernelGGL((decode_bundled_kernel<G, F, true, true>), grid, dim3(kThreads), 0, s, p.plan, p.B, p.Hkv, p.bundles, p);
+                    else hipLaunchKernelGGL((decode_bundled_kernel<G, F, false, true>), grid, dim3(kThreads), 0, s, p.plan, p.B, p.Hkv, p.bundles, p);
                 }
             } else if (p.stream) {
-                hipLaunchKernelGGL((decode_bundled_kernel<G, F, true, false>), grid, dim3(kThreads), 0, s, p);
+                hipLaunchKernelGGL((decode_bundled_kernel<G, F, true, false>), grid, dim3(kThreads), 0, s, p.plan, p.B, p.Hkv, p.bundles, p);
             } else {
-                hipLaunchKernelGGL((decode_bundled_kernel<G, F, false, false>), grid, dim3(kThreads), 0, s, p);
+                hipLaunchKernelGGL((decode_bundled_kernel<G, F, false, false>), grid, dim3(kThreads), 0, s, p.plan, p.B, p.Hkv, p.bundles, p);
             }
             return;
         }
