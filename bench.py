@@ -486,11 +486,11 @@ def main():
                       row[..., (HQ + HKV) * D:].view(BATCH, 1, HKV, D),
                       arena[layer], arena[LAYERS + layer], out[layer]))
 
-    plan_buf = torch.empty(BATCH, 2, device=device, dtype=torch.int32)
+    plan_buf = torch.empty(pkg.plan_shape(BATCH, HQ, HKV), device=device, dtype=torch.int32)
 
     def step():
         # one ranking per step (all layers attend the same lengths), inside the timed graph
-        plan = None if args.no_plan else pkg.decode_plan(positions, CAPACITY, out=plan_buf)
+        plan = None if args.no_plan else pkg.decode_plan(positions, CAPACITY, HQ, HKV, out=plan_buf)
         for q, k, v, ak, av, o in views:
             pkg.decode_step(q, k, v, ak, av, positions, cos, sin, out=o, max_chunks=args.max_chunks,
                             splits=args.splits, grid=args.grid, plan=plan)
@@ -526,7 +526,7 @@ def main():
                          splits=args.splits, grid=args.grid)
     torch.cuda.synchronize()
     with torch.cuda.graph(attn_graph):
-        plan = None if args.no_plan else pkg.decode_plan(positions, CAPACITY, out=plan_buf)
+        plan = None if args.no_plan else pkg.decode_plan(positions, CAPACITY, HQ, HKV, out=plan_buf)
         for layer in range(LAYERS):
             pkg.decode_attention(q0, arena[layer], arena[LAYERS + layer], positions,
                                  out=out[layer], max_chunks=args.max_chunks, splits=args.splits,

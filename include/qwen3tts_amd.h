@@ -120,11 +120,16 @@ int q3t_rope_tables(const int64_t *positions, int64_t n, const float *inv_freq, 
  * nothing and get zero rows.  Query head hq reads KV head hq / (q_heads / kv_heads).
  *
  * Three grids compute the same result (to rounding; `grid` picks one, Q3T_GRID_*):
- *   - bundled: one workgroup per CU, each owning a bundle of whole requests of one KV head
- *     (requests ranked by length, longest paired with shortest), streamed through LDS and
- *     scored on bf16 MFMA tiles; no workspace traffic.  bf16, head_dim 128, query_len 1, no
- *     mask, q_heads / kv_heads <= 4, batch <= 128.  The default for 64..128 requests (times
- *     kv_heads >= 512) over 1024 <= ctx < 2048 (the talker's 1024-row arena).
+ *   - bundled: one workgroup per CU, streaming keys through LDS and scoring them on bf16
+ *     MFMA tiles.  Unmasked, each workgroup takes whole requests, longest paired with
+ *     shortest, ranked by the step's `plan` (q3t_decode_plan) or, without one, by the
+ *     workgroup itself.  Masked (unit key stride, 4-byte aligned; the call must bring the
+ *     plan), each workgroup streams an equal share of one KV head's concatenated keys, every
+ *     request of the share scored at once as its own MFMA columns, and the requests cut
+ *     between shares merge through `workspace`.  bf16, head_dim 128, query_len 1,
+ *     q_heads / kv_heads <= 4, batch <= 128.  The
+ *     default for 64..128 requests (times kv_heads >= 512) over 1024 <= ctx < 2048 (the
+ *     talker's 1024-row arena).
  *   - balanced (`splits` workgroups per KV head): the concatenated keys of all requests of a
  *     head cut into equal shares, one per workgroup; the default for ctx >= 2048.
  *   - chunked: each request's keys cut into chunks of 64-key blocks (at most `max_chunks`
@@ -196,10 +201,15 @@ typedef struct q3t_decode_args {
     /* Q3T_GRID_AUTO (0), Q3T_GRID_CHUNKED, Q3T_GRID_BALANCED or Q3T_GRID_BUNDLED; a grid the
        call does not qualify for returns Q3T_EUNSUPPORTED */
     int64_t grid;
-    /* bundled grid, optional: the ranking q3t_decode_plan wrote for these `positions`, `batch`
-       and `ctx` (device, 2 * batch int32); the launch then skips its own ranking.  A plan made
-       for other positions gives wrong outputs (never accesses outside the arguments' ranges).
-       Ignored by the other grids; NULL = rank in the launch. */
+    /* bundled grid, optional (required with a mask): the plan q3t_decode_plan wrote for these
+       `positions`, `batch`, `ctx`, `q_heads` and `kv_heads` (device, q3t_decode_plan_bytes).
+       A masked launch streams the plan's equal shares of each KV head's keys (requests cut
+       between shares are merged through the workspace); an unmasked one takes whole requests
+       in the plan's ranking instead of ranking them itself.  A plan made for other positions
+       gives wrong outputs and writes the new K/V rows at the plan's rows, never outside the
+       arena.  One made for another batch gives NaN rows masked and is not used unmasked (the
+       launch ranks by itself); one for another ctx or head shape gives NaN rows masked.
+       Ignored by the other grids. */
     const int32_t *plan;
 } q3t_decode_args;
 
@@ -230,15 +240,29 @@ int q3t_decode_grid(const q3t_decode_args *args);
    time on one GPU (on two streams) race. */
 int q3t_decode_attention_static(const q3t_decode_args *args, void *stream);
 
-/* The bundled grid's ranking of a step's requests, written once per step and passed as
-   `plan` to every layer's launch of that step (the talker's layers all attend the same
-   lengths): plan[2r], plan[2r + 1] = b, L_b for the request b of rank r, with L_b =
-   positions[b] + 1 for a position in [0, ctx) and 0 otherwise, ranked by L_b descending, ties
-   by ascending b.  batch <= 128, ctx <= 2^20; `plan` holds 2 * batch int32 (8-byte aligned).
-   One small kernel on `stream`; it may be captured.  No counterpart in the reference (its
-   attention operator takes no per-step state; positions are fixed for a step's layers in
-   SlotGraph.compute, continuous.py:188-198). */
-int q3t_decode_plan(const int64_t *positions, int64_t batch, int64_t ctx, int32_t *plan, void *stream);
+/* The bundled grid's plan of a step, written once per step and passed as `plan` to every
+   layer's launch of that step (the talker's layers all attend the same lengths).  With
+   L_b = positions[b] + 1 for a position in [0, ctx) and 0 otherwise, the keys of all requests
+   laid end to end in request order are cut into M shares of whole 64-key stages (M =
+   max(ceil(256 / kv_heads), ceil(batch / 4)) per KV head, one workgroup per CU); share m's
+   entries are up to 8 segments (request b, keys [j0, j1), flags) at int32 offset 32 m, and a
+   header of 32 ints (batch, M, segments per share, ctx, bit mask of requests with L_b = 0,
+   zeros) follows the M shares.  A share holds at most min(8, 16 / (q_heads / kv_heads))
+   segments and a request spans at most three shares; positions that need more get whole
+   requests paired longest with shortest instead.  The ranking section follows the header:
+   (batch, 0), then the pairs (b, L_b) of ranks 0 .. 127, longest first with ties by ascending
+   b ((-1, 0) past the batch); unmasked launches read it, masked ones the shares.
+   batch <= 128, ctx <= 2^20, q_heads / kv_heads in {1, 2, 4};
+   `plan` holds q3t_decode_plan_bytes bytes (16-byte aligned).  One small kernel on `stream`;
+   it may be captured.  No counterpart in the reference (its attention operator takes no
+   per-step state; positions are fixed for a step's layers in SlotGraph.compute,
+   continuous.py:188-198). */
+int q3t_decode_plan(const int64_t *positions, int64_t batch, int64_t ctx, int64_t q_heads, int64_t kv_heads,
+                    int32_t *plan, void *stream);
+
+/* Bytes of the plan q3t_decode_plan writes for this launch shape; -1 for a shape it does not
+   plan.  No counterpart in the reference. */
+int64_t q3t_decode_plan_bytes(int64_t batch, int64_t q_heads, int64_t kv_heads);
 
 /* Re-zero the counter region of a decode workspace on `stream` (a kernel, so it may be
    captured).  Every completed launch leaves the counters zeroed; a launch that failed

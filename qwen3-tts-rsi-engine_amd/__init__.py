@@ -25,7 +25,7 @@ from .packed_kv import copy_packed_prefix, copy_rows
 from .kv_write import write, write_tokens
 from .rotary import rotary, rope_tables, inverse_frequencies
 from .attention import (attention, decode_attention, decode_step, decode_grid_for, decode_plan,
-                        prefill_attention)
+                        plan_shape, prefill_attention, reset_workspaces)
 from .prefill import prefill_rope_write, prefill_step
 from .packed_attention import PackedAttention, install_packed_attention, restore_modules
 from .scheduler import SlotScheduler, DecodeBatch
@@ -37,6 +37,7 @@ __all__ = [
     "decode_batch_size", "copy_packed_prefix", "copy_rows", "write", "write_tokens", "rotary",
     "rope_tables", "inverse_frequencies", "attention", "decode_attention", "decode_step", "decode_grid_for",
     "decode_plan",
+    "plan_shape", "reset_workspaces",
     "prefill_attention", "prefill_rope_write", "prefill_step", "PackedAttention",
     "install_packed_attention", "restore_modules", "SlotScheduler", "DecodeBatch", "SlotArena",
     "SlotCache", "PredictorCache", "PrefillCache", "grow_arena", "SlotGraph", "PrefillGraph",

@@ -103,7 +103,8 @@ SIGNATURES = {
     "q3t_decode_grid": (ctypes.c_int, [ctypes.POINTER(DecodeArgs)]),
     "q3t_decode_attention": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
     "q3t_decode_reset_workspace": (ctypes.c_int, [c_vp, c_i64, c_vp]),
-    "q3t_decode_plan": (ctypes.c_int, [c_vp, c_i64, c_i64, c_vp, c_vp]),
+    "q3t_decode_plan": (ctypes.c_int, [c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp]),
+    "q3t_decode_plan_bytes": (ctypes.c_int64, [c_i64, c_i64, c_i64]),
     "q3t_decode_attention_static": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
     "q3t_prefill_attention": (ctypes.c_int, [ctypes.POINTER(PrefillArgs), c_vp]),
     "q3t_prefill_rope_write": (ctypes.c_int, [ctypes.POINTER(PrefillRopeWriteArgs), c_vp]),
@@ -117,7 +118,7 @@ class KernelError(RuntimeError):
     """A HIP launch failed after host validation passed."""
 
 
-ABI_VERSION = 6  # q3t_abi_version() of the header these structures mirror
+ABI_VERSION = 7  # q3t_abi_version() of the header these structures mirror
 
 
 def library() -> ctypes.CDLL:

@@ -117,14 +117,22 @@ def _grid_code(grid):
 
 
 def decode_grid_for(batch, query_len, q_heads, kv_heads, head_dim, ctx, dtype=torch.bfloat16, *,
-                    masked=False, splits=0, grid=None):
+                    masked=False, splits=0, grid=None, planned=True):
     """Name of the grid a decode call of these sizes runs on ('bundled', 'balanced' or
     'chunked'), as the library chooses it (q3t_decode_grid); ValueError when a named grid does
-    not take such a call."""
+    not take such a call.  ``masked``: a contiguous (batch, 1, ctx) bf16 mask, as
+    SlotGraph.compute builds it; ``planned``: the call brings the step's ``decode_plan`` (the
+    slot cache's talker step does)."""
     a = _lib.DecodeArgs()
     a.batch, a.query_len, a.q_heads, a.kv_heads, a.head_dim, a.ctx = batch, query_len, q_heads, kv_heads, head_dim, ctx
     a.dtype = _lib.DTYPE_CODES[dtype]
-    a.mask = 16 if masked else None
+    a.k_stride_b = a.v_stride_b = kv_heads * ctx * head_dim
+    a.k_stride_h = a.v_stride_h = ctx * head_dim
+    a.k_stride_t = a.v_stride_t = head_dim
+    if masked:
+        a.mask, a.mask_dtype = 16, _lib.Q3T_BF16
+        a.mask_stride_b, a.mask_stride_s, a.mask_stride_t = ctx, ctx, 1
+    a.plan = 16 if planned else None
     a.splits, a.grid = int(splits), _grid_code(grid)
     code = _lib.library().q3t_decode_grid(a)
     if code < 0:
@@ -132,48 +140,67 @@ def decode_grid_for(batch, query_len, q_heads, kv_heads, head_dim, ctx, dtype=to
     return {v: k for k, v in GRIDS.items() if k not in (None, 'auto')}[code]
 
 
-PLAN_MAX_BATCH = 128  # requests a decode plan ranks (the bundled grid's limit)
+PLAN_MAX_BATCH = 128  # requests a decode plan covers (the bundled grid's limit)
 
 
-def decode_plan(positions, capacity, *, out=None):
-    """The bundled grid's ranking of a step's requests, made once for the step's positions
-    and passed as ``plan=`` to every layer's ``decode_step`` / ``decode_attention`` of that step
-    (the layers of a talker step all attend the same lengths, SlotGraph.compute,
-    continuous.py:188-198), so that no launch ranks the requests itself.  positions (B,) int64
-    with B <= 128, capacity: the arena's rows (the launches' ctx).  Returns an int32 (B, 2)
-    tensor of (request, keys) pairs, longest first (ties by request index); a request without
-    a position in [0, capacity) has 0 keys.  One small kernel on the current stream (it can be
-    captured); the plan stays valid while ``positions`` and ``capacity`` are unchanged: a plan
-    of other positions gives wrong outputs."""
+def plan_shape(batch, q_heads, kv_heads):
+    """Shape of the int32 plan ``decode_plan`` writes for a launch of these sizes: one
+    dimension holding (shares, 8, 4) segment entries of every KV head's shares, a header of 32
+    ints and a ranking section of 258 ints (q3t_decode_plan); None when no plan covers the
+    shape."""
+    nbytes = _lib.library().q3t_decode_plan_bytes(int(batch), int(q_heads), int(kv_heads))
+    if nbytes <= 0:
+        return None
+    return (nbytes // 4,)
+
+
+def decode_plan(positions, capacity, q_heads, kv_heads, *, out=None):
+    """The bundled grid's plan of a step, made once for the step's positions and passed as
+    ``plan=`` to every layer's ``decode_step`` / ``decode_attention`` of that step (the layers
+    of a talker step all attend the same lengths, SlotGraph.compute, continuous.py:188-198).
+    positions (B,) int64 with B <= 128, capacity: the arena's rows (a position at or past it
+    attends nothing), q_heads / kv_heads: the attention's heads (q_heads / kv_heads in
+    {1, 2, 4}).  The plan holds two cuts of the step's keys.  A masked launch reads the first:
+    the keys of all requests, end to end in request order, cut into equal shares of whole
+    64-key stages, one per workgroup of each KV head, a request cut between shares merged
+    through the launch's workspace.  An unmasked launch reads the second: the requests ranked
+    by length, whole requests per workgroup paired longest with shortest.  Returns an int32
+    ``plan_shape`` tensor.
+    One small kernel on the current stream (it can be captured); the plan stays valid while
+    ``positions`` are unchanged: a plan of other positions gives wrong outputs."""
     if positions.ndim != 1 or positions.dtype != torch.int64:
         raise ValueError('positions must be an int64 (batch,) tensor')
     batch = positions.shape[0]
     if batch > PLAN_MAX_BATCH:
-        raise ValueError(f'a decode plan ranks at most {PLAN_MAX_BATCH} requests')
+        raise ValueError(f'a decode plan covers at most {PLAN_MAX_BATCH} requests')
     if not 1 <= int(capacity) <= 1 << 20:
         raise ValueError('capacity must be in [1, 2^20]')
+    shape = plan_shape(batch, q_heads, kv_heads)
+    if shape is None:
+        raise ValueError('a decode plan needs q_heads / kv_heads in {1, 2, 4}')
     device = _lib.require_gpu(positions)
     if not positions.is_contiguous():
         positions = positions.contiguous()
     if out is None:
-        out = torch.empty(batch, 2, device=device, dtype=torch.int32)
+        out = torch.empty(shape, device=device, dtype=torch.int32)
     else:
-        _check_out(out, (batch, 2), torch.int32, device, 'decode plan')
+        _check_out(out, shape, torch.int32, device, 'decode plan')
         if not out.is_contiguous():
             raise ValueError('decode plan: out must be contiguous')
     with torch.cuda.device(device):
-        status = _lib.library().q3t_decode_plan(positions.data_ptr(), batch, int(capacity), out.data_ptr(),
-                                                _lib.stream_handle(device))
+        status = _lib.library().q3t_decode_plan(positions.data_ptr(), batch, int(capacity), int(q_heads),
+                                                int(kv_heads), out.data_ptr(), _lib.stream_handle(device))
     _lib.check(status, 'decode plan')
     return out
 
 
-def _set_plan(a, plan, batch, device):
+def _set_plan(a, plan, device):
     if plan is None:
         return
-    if (plan.shape != (batch, 2) or plan.dtype != torch.int32 or not plan.is_contiguous()
+    shape = plan_shape(a.batch, a.q_heads, a.kv_heads)
+    if (shape is None or tuple(plan.shape) != shape or plan.dtype != torch.int32 or not plan.is_contiguous()
             or plan.device != device):
-        raise ValueError(f'plan must be the contiguous int32 ({batch}, 2) tensor of decode_plan on {device}')
+        raise ValueError(f'plan must be the contiguous int32 {shape} tensor of decode_plan on {device}')
     a.plan = plan.data_ptr()
 
 
@@ -182,15 +209,17 @@ def decode_attention(query, keys, values, positions, *, scale=None, mask=None, k
     """query (B, S, Hq, D) BSND; keys/values (B, Hkv, ctx, D) views of the arena (or, with
     ``kv_offsets``, any base tensor whose request rows start at those element offsets);
     positions (B,) int64: the last query position of each request.  ``grid`` picks the
-    kernel grid: 'bundled' (whole requests in length-balanced bundles, one workgroup per CU,
-    bf16 MFMA tiles; one query token, head_dim 128, no mask, up to 128 requests), 'balanced'
+    kernel grid: 'bundled' (one workgroup per CU streaming through LDS onto bf16 MFMA tiles: with
+    a mask and ``plan``, equal shares of each head's keys; without a mask, whole requests in
+    length-balanced bundles, ranked by ``plan`` when given; one query token, head_dim 128, up to
+    128 requests), 'balanced'
     (equal shares of each head's keys over ``splits`` workgroups per head, 0: 256 in all),
     'chunked' (chunks of 64-key blocks per request, at most ``max_chunks``, 0: enough for
     ~512 workgroups) or None for the library's choice, in which ``splits`` > 0 / < 0 still
     selects balanced / chunked.  ``no_alloc`` runs the library's allocation-free entry point, which keeps
     its split states in a fixed per-GPU device array instead of a workspace (calls that
-    overlap in time on one GPU then race).  ``plan``: ``decode_plan(positions, ctx)`` of these
-    positions; the bundled grid then skips its own ranking (other grids ignore it).
+    overlap in time on one GPU then race).  ``plan``: ``decode_plan(positions, ctx, q_heads,
+    kv_heads)`` of these positions, read by the bundled grid (other grids ignore it).
     Returns (B, S, Hq, D)."""
     if query.ndim != 4 or keys.ndim != 4 or values.shape != keys.shape:
         raise ValueError('expected BSND query and BNSD key/value views')
@@ -238,7 +267,7 @@ def decode_attention(query, keys, values, positions, *, scale=None, mask=None, k
     a.max_chunks = int(max_chunks)
     a.splits = int(splits)
     a.grid = _grid_code(grid)
-    _set_plan(a, plan, batch, device)
+    _set_plan(a, plan, device)
     _run_decode(a, device, 'decode attention', no_alloc)
     return out
 
@@ -264,7 +293,7 @@ def decode_step(query, new_key, new_value, key_arena, value_arena, positions, co
     0 ... positions[b], as the reference's operator applies the mask it is given; without it
     request b attends exactly those keys (the ``j <= pos[b]`` mask of SlotGraph.compute).
     ``grid`` / ``splits`` / ``max_chunks`` choose the grid, ``no_alloc`` the
-    allocation-free entry point and ``plan`` the step's ranking, as in ``decode_attention``."""
+    allocation-free entry point and ``plan`` the step's plan, as in ``decode_attention``."""
     if (query.ndim != 4 or query.shape[1] not in (1, 2) or new_key.ndim != 4
             or new_key.shape[1] != query.shape[1]):
         raise ValueError('fused decode expects one- or two-token BSND rows')
@@ -335,7 +364,7 @@ def decode_step(query, new_key, new_value, key_arena, value_arena, positions, co
         _lib.require_gpu(weight)
         setattr(a, name, weight.data_ptr())
     a.norm_eps = float(norm_eps)
-    _set_plan(a, plan, batch, device)
+    _set_plan(a, plan, device)
     _run_decode(a, device, 'fused decode step', no_alloc)
     return out
 

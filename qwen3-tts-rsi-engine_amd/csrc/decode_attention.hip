@@ -27,7 +27,7 @@
 //   * a (request, head) covered by several workgroups combines their states through the
 //     workspace (finish_split): the last one to arrive merges in part order, writes the
 //     output and re-zeroes the pair's counter, so launches can be replayed from a graph.
-#include "q3t_common.hpp"
+#include "decode_params.hpp"
 
 #include <mutex>
 
@@ -41,46 +41,6 @@ constexpr int kWaves = kThreads / 64;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kEmpty = -1.0e30f;  // finite "no key yet" running max
 constexpr int kMinShare = 32;       // balanced grid: fewest keys per workgroup
-
-struct DecodeParams {
-    int B, Hq, Hkv, ctx, nchunks;
-    int splits;             // balanced grid: workgroups per KV head (0: chunked grid)
-    int bundles;            // bundled grid: workgroups per KV head (0: another grid)
-    float scale_log2;
-    int has_mask, mask_dtype;
-    const char *q;
-    int64_t q_sb, q_ss, q_sh;
-    char *k, *v;
-    int64_t k_sb, k_sh, k_st, v_sb, v_sh, v_st;
-    const int64_t *offs;
-    const int64_t *pos;
-    const char *mask;
-    int64_t m_sb, m_ss, m_st;
-    char *out;
-    int64_t o_sb, o_ss, o_sh;
-    const char *nk, *nv;
-    int64_t nk_sb, nk_sh, nv_sb, nv_sh;
-    const char *cs, *sn;
-    int64_t cs_sb;
-    float *partials;
-    int *counters;
-    const char *qnw, *knw;  // fused: optional RMSNorm weights (bf16, D) of query / new key rows
-    float eps;
-    int stream;             // read K/V rows with the non-temporal cache policy (host choice)
-    int64_t nk_ss, nv_ss, cs_ss;  // fused, two tokens: token strides of new K/V and cos/sin
-    const int32_t *plan;    // bundled grid, optional: (b, L) pairs ranked longest first
-};
-
-Q3T_DEVICE int mask_elem_size(int dtype) { return dtype == Q3T_F32 ? 4 : dtype == Q3T_BOOL ? 1 : 2; }
-
-Q3T_DEVICE float load_mask(const char *m, int dtype) {
-    switch (dtype) {
-        case Q3T_BF16: return bf16_to_float(*reinterpret_cast<const uint16_t *>(m));
-        case Q3T_F16: return (float)*reinterpret_cast<const _Float16 *>(m);
-        case Q3T_F32: return *reinterpret_cast<const float *>(m);
-        default: return *reinterpret_cast<const uint8_t *>(m) ? 0.0f : -INFINITY;  // bool: True attends
-    }
-}
 
 // Partial score of one lane: its 16 bytes of the query row and of the key row.
 template <typename T>
@@ -898,32 +858,37 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(const int32_t 
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS bases stay scalar
     const int h = blockIdx.x % hkv, m = blockIdx.x / hkv, M = bundles;
-    // The plan entries of this bundle and every line of the argument block in one scalar round
-    // trip: the plan pointer and the sizes its addresses need are the leading kernel arguments,
-    // which the hardware preloads into scalar registers.
+    // The plan entries of this bundle, the plan's batch and every line of the argument block in
+    // one scalar round trip: the plan pointer and the sizes its addresses need are the leading
+    // kernel arguments, which the hardware preloads into scalar registers.  The plan's ranking
+    // section is (B, 0) and then the (b, L) pair of each rank.
     auto bundle_rank = [&](int i) { return (i >> 1) * 2 * M + ((i & 1) ? 2 * M - 1 - m : m); };
     uint64_t e[kBundleMaxSeg] = {0, 0, 0, 0};
+    uint32_t plan_batch = 0;
     if (plan) {
         const uint64_t base = reinterpret_cast<uint64_t>(plan);
         uint64_t a[kBundleMaxSeg];
 #pragma unroll
         for (int i = 0; i < kBundleMaxSeg; ++i)
-            a[i] = base + 8 * (uint64_t)(bundle_rank(i) < nb ? bundle_rank(i) : 0);
+            a[i] = base + 8 + 8 * (uint64_t)(bundle_rank(i) < nb ? bundle_rank(i) : 0);
         constexpr int BYTES = 32 + (int)sizeof(DecodeParams);
         static_assert(BYTES <= 8 * 64, "eight 64-byte lines at most");
         const uint64_t ka = reinterpret_cast<uint64_t>(__builtin_amdgcn_kernarg_segment_ptr());
         uint32_t d0, d1, d2, d3, d4, d5, d6, d7;
-        asm volatile("s_load_dwordx2 %0, %12, 0x0\n\ts_load_dwordx2 %1, %13, 0x0\n\t"
-                     "s_load_dwordx2 %2, %14, 0x0\n\ts_load_dwordx2 %3, %15, 0x0\n\t"
-                     "s_load_dword %4, %16, 0x0\n\ts_load_dword %5, %16, 0x40\n\t"
-                     "s_load_dword %6, %16, 0x80\n\ts_load_dword %7, %16, 0xc0\n\t"
-                     "s_load_dword %8, %16, %17\n\ts_load_dword %9, %16, %18\n\t"
-                     "s_load_dword %10, %16, %19\n\ts_load_dword %11, %16, %20\n\t"
+        asm volatile("s_load_dwordx2 %[e0], %[a0], 0x0\n\ts_load_dwordx2 %[e1], %[a1], 0x0\n\t"
+                     "s_load_dwordx2 %[e2], %[a2], 0x0\n\ts_load_dwordx2 %[e3], %[a3], 0x0\n\t"
+                     "s_load_dword %[nb], %[base], 0x0\n\t"
+                     "s_load_dword %[d0], %[ka], 0x0\n\ts_load_dword %[d1], %[ka], 0x40\n\t"
+                     "s_load_dword %[d2], %[ka], 0x80\n\ts_load_dword %[d3], %[ka], 0xc0\n\t"
+                     "s_load_dword %[d4], %[ka], %[o4]\n\ts_load_dword %[d5], %[ka], %[o5]\n\t"
+                     "s_load_dword %[d6], %[ka], %[o6]\n\ts_load_dword %[d7], %[ka], %[o7]\n\t"
                      "s_waitcnt lgkmcnt(0)"
-                     : "=&s"(e[0]), "=&s"(e[1]), "=&s"(e[2]), "=&s"(e[3]), "=&s"(d0), "=&s"(d1), "=&s"(d2),
-                       "=&s"(d3), "=&s"(d4), "=&s"(d5), "=&s"(d6), "=&s"(d7)
-                     : "s"(a[0]), "s"(a[1]), "s"(a[2]), "s"(a[3]), "s"(ka), "n"(BYTES > 0x100 ? 0x100 : 0),
-                       "n"(BYTES > 0x140 ? 0x140 : 0), "n"(BYTES > 0x180 ? 0x180 : 0), "n"(BYTES > 0x1c0 ? 0x1c0 : 0)
+                     : [e0] "=&s"(e[0]), [e1] "=&s"(e[1]), [e2] "=&s"(e[2]), [e3] "=&s"(e[3]),
+                       [nb] "=&s"(plan_batch), [d0] "=&s"(d0), [d1] "=&s"(d1), [d2] "=&s"(d2), [d3] "=&s"(d3),
+                       [d4] "=&s"(d4), [d5] "=&s"(d5), [d6] "=&s"(d6), [d7] "=&s"(d7)
+                     : [a0] "s"(a[0]), [a1] "s"(a[1]), [a2] "s"(a[2]), [a3] "s"(a[3]), [base] "s"(base),
+                       [ka] "s"(ka), [o4] "n"(BYTES > 0x100 ? 0x100 : 0), [o5] "n"(BYTES > 0x140 ? 0x140 : 0),
+                       [o6] "n"(BYTES > 0x180 ? 0x180 : 0), [o7] "n"(BYTES > 0x1c0 ? 0x1c0 : 0)
                      : "memory");
     } else {
         prefetch_kernargs<32 + sizeof(DecodeParams)>();
@@ -951,11 +916,11 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(const int32_t 
         tb_v.set(i, (p.offs ? o : (int64_t)b * p.v_sb) + h * p.v_sh);
         nseg = i + 1;
     };
-    if (plan) {
+    if (plan && (int)plan_batch == nb) {
         // a ranking made once for the step's positions (q3t_decode_plan): (b, L) pairs, longest
         // first, loaded above; no ranking here.  Entries that do not name a request of this
         // batch attend nothing and write nothing (ranks past the batch read entry 0 and are
-        // ignored).
+        // ignored).  A plan made for another batch is not used: the launch ranks by itself.
 #pragma unroll
         for (int i = 0; i < kBundleMaxSeg; ++i) {
             if (bundle_rank(i) >= p.B) continue;
@@ -1312,37 +1277,6 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(const int32_t 
     }
 }
 
-// The ranking the bundled grid works from, made once for a step's positions and read by every
-// layer's launch of that step (all layers of a talker step attend the same lengths): plan[r] =
-// (b, L_b) for the request b of rank r, L_b = pos[b] + 1 for a position in [0, ctx) and 0
-// otherwise, ranked by L descending with ties by ascending b.  One workgroup: thread t ranks
-// request t % 128 against half t / 128 of the keys (broadcast LDS reads), the halves add up.
-constexpr int kPlanThreads = 2 * kBundleMaxBatch;
-__global__ void __launch_bounds__(kPlanThreads) decode_plan_kernel(const int64_t *pos, int B, int ctx, int2 *plan) {
-    __shared__ __attribute__((aligned(16))) int keys[kBundleMaxBatch];
-    __shared__ int part[kPlanThreads];
-    const int t = threadIdx.x, b = t % kBundleMaxBatch, half = t / kBundleMaxBatch;
-    int L = 0;
-    if (b < B) {
-        const int64_t pb = pos[b];
-        L = (pb >= 0 && pb < ctx) ? (int)pb + 1 : 0;
-    }
-    // ctx <= 2^20 keeps L << 7 below 2^31; b < 128 fits the low 7 bits
-    const int key = b < B ? (L << 7) | (kBundleMaxBatch - 1 - b) : -1;
-    if (half == 0) keys[b] = key;
-    __syncthreads();
-    int rank = 0;
-    constexpr int kHalf = kBundleMaxBatch / 2;
-#pragma unroll
-    for (int j = 0; j < kHalf / 4; ++j) {
-        const i32x4_t k4 = *(const i32x4_t *)&keys[half * kHalf + 4 * j];
-        rank += (k4.x > key) + (k4.y > key) + (k4.z > key) + (k4.w > key);
-    }
-    part[t] = rank;
-    __syncthreads();
-    if (half == 0 && b < B) plan[rank + part[t + kBundleMaxBatch]] = int2{b, L};
-}
-
 // ---------------------------------------------------------------------------------------
 
 // The counter region has one fixed size, so that the counters of every launch sit on bytes
@@ -1385,8 +1319,9 @@ static int64_t chunk_count(int64_t batch, int64_t kv_heads, int64_t ctx, int64_t
 }
 
 // The grid a call runs on (Q3T_GRID_CHUNKED, _BALANCED or _BUNDLED; -1: a requested grid the
-// call does not qualify for).  The bundled grid needs bf16 rows of 128, one query token, no
-// mask, at most kBundleMaxBatch requests and q_heads / kv_heads <= 4.  Automatic choice,
+// call does not qualify for).  The bundled grid needs bf16 rows of 128, one query token, at
+// most kBundleMaxBatch requests, q_heads / kv_heads <= 4, and a mask only where the shares
+// kernel takes the call.  Automatic choice,
 // measured (bf16, 16/8 heads, fused and unfused): bundled for 64..128 requests over arenas of
 // 1024 to 2047 rows (64 requests over 1024 rows: 27.6 us against 30.0 chunked and 37.9
 // balanced; 128 requests: 50.4 against 52.1 and 54.8); balanced from 2048 rows (128 requests
@@ -1394,8 +1329,28 @@ static int64_t chunk_count(int64_t batch, int64_t kv_heads, int64_t ctx, int64_t
 // fewer requests (128 requests over 512 rows: 32.0 against 33.9 bundled; 32 over 1024: 21.6
 // against 21.8), where the bundled grid's ranking and start-up are not repaid.
 constexpr int64_t kBundleMinCtx = 1024;
+// A masked bundled launch runs the shares kernel (decode_shares.hip), an unmasked one the
+// whole-request kernel above.  The shares kernel takes a call that brings the step's plan
+// (q3t_decode_plan) and whose arena rows can be addressed from one base per KV head: no
+// per-request offsets, identical key and value layouts, and every request's rows of a head
+// within 4 GiB of request 0's; a mask needs unit key stride and 4-byte alignment.
+static bool shares_ok(const q3t_decode_args *a) {
+    if (!a->plan || a->kv_offsets || a->k_stride_b != a->v_stride_b || a->k_stride_h != a->v_stride_h ||
+        a->k_stride_t != a->v_stride_t || a->k_stride_b < 0 || a->k_stride_t < 0)
+        return false;
+    const int64_t g = a->q_heads / a->kv_heads;
+    if (g != 1 && g != 2 && g != 4) return false;
+    if ((a->batch - 1) * a->k_stride_b * 2 + (a->ctx - 1) * a->k_stride_t * 2 + 256 > (int64_t)UINT32_MAX) return false;
+    if (shares_flag_count(a->batch, a->kv_heads) > kMaxCounters) return false;
+    if (a->mask) {
+        const int64_t es = a->mask_dtype == Q3T_F32 ? 4 : a->mask_dtype == Q3T_BOOL ? 1 : 2;
+        if (a->mask_stride_t != 1 || a->mask_stride_b < 0 || !aligned(a->mask, 4)) return false;
+        if (((a->batch - 1) * a->mask_stride_b + a->ctx) * es + 3 > (int64_t)INT32_MAX) return false;
+    }
+    return true;
+}
 static bool bundle_ok(const q3t_decode_args *a) {
-    return a->dtype == Q3T_BF16 && a->head_dim == 128 && a->query_len == 1 && !a->mask &&
+    return a->dtype == Q3T_BF16 && a->head_dim == 128 && a->query_len == 1 && (!a->mask || shares_ok(a)) &&
            a->batch <= kBundleMaxBatch && a->q_heads / a->kv_heads <= 4;
 }
 static int decode_grid(const q3t_decode_args *a) {
@@ -1422,6 +1377,7 @@ static int64_t balanced_splits(const q3t_decode_args *a) {
 // Bundled grid: bundles (workgroups) per KV head, one workgroup per CU in all, and at most
 // kBundleMaxSeg requests per bundle.
 static int64_t bundle_count(const q3t_decode_args *a) {
+    if (a->mask) return shares_bundle_count(a->batch, a->kv_heads);
     const int64_t m = (kBundleGroups + a->kv_heads - 1) / a->kv_heads;
     const int64_t least = (a->batch + kBundleMaxSeg - 1) / kBundleMaxSeg;
     return m < least ? least : m;
@@ -1435,7 +1391,9 @@ static int64_t partial_floats(const q3t_decode_args *a) {
         case Q3T_GRID_CHUNKED:
             units = a->batch * a->kv_heads * chunk_count(a->batch, a->kv_heads, a->ctx, a->max_chunks);
             break;
-        default: break;  // bundled: no partial states
+        case Q3T_GRID_BUNDLED:  // the shares grid publishes the states of requests cut between shares
+            return a->mask && shares_ok(a) ? shares_partial_floats(a->batch, a->kv_heads, a->q_heads / a->kv_heads) : 0;
+        default: break;
     }
     return units * R * (a->head_dim + 2);
 }
@@ -1484,18 +1442,26 @@ static void launch_split(const DecodeParams &p, hipStream_t s) {
 
 template <typename T, int D, int G, int SQ, bool F, bool M>
 static void launch_decode(const DecodeParams &p, hipStream_t s) {
+    if constexpr (sizeof(T) == 2 && D == 128 && SQ == 1 && M && G <= 4) {
+        if (p.bundles > 0 && p.plan) {  // a mask: the shares grid
+            shares_launch(p, G, F, F && (p.qnw || p.knw), M, s);
+            return;
+        }
+    }
     if constexpr (sizeof(T) == 2 && D == 128 && SQ == 1 && !M && G <= 4) {
         if (p.bundles > 0) {
+            // whole requests per workgroup; with the step's plan, its ranking section
+            const int32_t *rank = p.plan ? p.plan + shares_rank_offset(p.B, p.Hkv) : nullptr;
             const dim3 grid((uint32_t)p.bundles * p.Hkv);
             if (F && (p.qnw || p.knw)) {
                 if constexpr (F) {
-                    if (p.stream) hipLaunchKernelGGL((decode_bundled_kernel<G, F, true, true>), grid, dim3(kThreads), 0, s, p.plan, p.B, p.Hkv, p.bundles, p);
-                    else hipLaunchKernelGGL((decode_bundled_kernel<G, F, false, true>), grid, dim3(kThreads), 0, s, p.plan, p.B, p.Hkv, p.bundles, p);
+                    if (p.stream) hipLaunchKernelGGL((decode_bundled_kernel<G, F, true, true>), grid, dim3(kThreads), 0, s, rank, p.B, p.Hkv, p.bundles, p);
+                    else hipLaunchKernelGGL((decode_bundled_kernel<G, F, false, true>), grid, dim3(kThreads), 0, s, rank, p.B, p.Hkv, p.bundles, p);
                 }
             } else if (p.stream) {
-                hipLaunchKernelGGL((decode_bundled_kernel<G, F, true, false>), grid, dim3(kThreads), 0, s, p.plan, p.B, p.Hkv, p.bundles, p);
+                hipLaunchKernelGGL((decode_bundled_kernel<G, F, true, false>), grid, dim3(kThreads), 0, s, rank, p.B, p.Hkv, p.bundles, p);
             } else {
-                hipLaunchKernelGGL((decode_bundled_kernel<G, F, false, false>), grid, dim3(kThreads), 0, s, p.plan, p.B, p.Hkv, p.bundles, p);
+                hipLaunchKernelGGL((decode_bundled_kernel<G, F, false, false>), grid, dim3(kThreads), 0, s, rank, p.B, p.Hkv, p.bundles, p);
             }
             return;
         }
@@ -1617,7 +1583,7 @@ static int decode_params(const q3t_decode_args *a, char *ws, DecodeParams &p) {
     p.qnw = nullptr;
     p.knw = nullptr;
     p.eps = a->norm_eps;
-    p.plan = grid == Q3T_GRID_BUNDLED ? a->plan : nullptr;  // only the bundled grid ranks requests
+    p.plan = grid == Q3T_GRID_BUNDLED ? a->plan : nullptr;  // read by the bundled grid's two kernels
     if (a->q_norm_weight || a->k_norm_weight) {
         if (!fused || !(a->norm_eps >= 0.f)) return Q3T_EINVAL;
         if ((a->q_norm_weight && !aligned(a->q_norm_weight, 16)) ||
@@ -1717,11 +1683,22 @@ extern "C" int q3t_decode_attention(const q3t_decode_args *a, void *stream) {
     return decode_launch(a, p, stream);
 }
 
-extern "C" int q3t_decode_plan(const int64_t *positions, int64_t batch, int64_t ctx, int32_t *plan, void *stream) {
-    if (batch < 0 || batch > kBundleMaxBatch || ctx < 1 || ctx > (1 << 20)) return Q3T_EINVAL;
+static bool plan_shape_ok(int64_t batch, int64_t ctx, int64_t q_heads, int64_t kv_heads) {
+    return batch >= 0 && batch <= kBundleMaxBatch && ctx >= 1 && ctx <= (1 << 20) && kv_heads >= 1 &&
+           q_heads >= kv_heads && q_heads % kv_heads == 0 &&
+           (q_heads / kv_heads == 1 || q_heads / kv_heads == 2 || q_heads / kv_heads == 4);
+}
+
+extern "C" int64_t q3t_decode_plan_bytes(int64_t batch, int64_t q_heads, int64_t kv_heads) {
+    if (!plan_shape_ok(batch, 1, q_heads, kv_heads)) return -1;
+    return shares_plan_ints(batch, kv_heads) * 4;
+}
+
+extern "C" int q3t_decode_plan(const int64_t *positions, int64_t batch, int64_t ctx, int64_t q_heads,
+                               int64_t kv_heads, int32_t *plan, void *stream) {
+    if (!plan_shape_ok(batch, ctx, q_heads, kv_heads)) return Q3T_EINVAL;
     if (batch == 0) return Q3T_OK;
-    if (!positions || !plan || !aligned(positions, 8) || !aligned(plan, 8)) return Q3T_EINVAL;
-    hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, (hipStream_t)stream, positions,
-                       (int)batch, (int)ctx, reinterpret_cast<int2 *>(plan));
-    return launch_status();
+    if (!positions || !plan || !aligned(positions, 8) || !aligned(plan, 16)) return Q3T_EINVAL;
+    return shares_plan_launch(positions, (int)batch, (int)ctx, (int)shares_bundle_count(batch, kv_heads),
+                              shares_slot_cap(q_heads / kv_heads), plan, (hipStream_t)stream);
 }

@@ -38,7 +38,7 @@ from __future__ import annotations
 
 import torch
 
-from .attention import attention, decode_step, prefill_attention
+from .attention import attention, decode_step, plan_shape, prefill_attention
 from .prefill import prefill_rope_write
 from .rotary import rotary
 from .slots import PredictorCache, PrefillCache, SlotCache
@@ -161,7 +161,7 @@ class PackedAttention(torch.nn.Module):
 
     def _fused_target(self, cache, attention_mask, batch, length, query):
         """(keys, values, positions, mask, plan) of a step the fused launch can take, else None
-        (plan: the slot cache's ranking of the step's requests, SlotCache.prepare).
+        (plan: the slot cache's plan of the step's requests, SlotCache.prepare).
 
         The mask the layer is given is applied in the launch (the reference's operator applies
         it, npu_attention.py:16-25), except the predictor's first-step 2x2 causal mask, which
@@ -231,8 +231,8 @@ class PackedAttention(torch.nn.Module):
         fused = self._fused_target(past_key_values, attention_mask, batch, length, query)
         if fused is not None:
             keys, values, positions, mask, plan = fused
-            if plan is not None and plan.shape[0] != batch:
-                plan = None
+            if plan is not None and tuple(plan.shape) != plan_shape(batch, query.shape[2], key.shape[2]):
+                plan = None  # a plan of another batch (a graph bucket the cache was not prepared for)
             if self._norms is not None and self._norms[0].device == query.device:
                 q_weight, k_weight, eps = self._norms
                 output = decode_step(query, key, value, keys, values, positions, cos, sin,

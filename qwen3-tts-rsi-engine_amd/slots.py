@@ -13,7 +13,7 @@ import torch
 from transformers.cache_utils import Cache
 
 from . import kv_write
-from .attention import PLAN_MAX_BATCH, decode_plan
+from .attention import PLAN_MAX_BATCH, decode_plan, plan_shape
 from .packed_kv import copy_packed_prefix, copy_rows
 
 
@@ -121,25 +121,27 @@ class SlotCache(Cache):
         self.context_length = arena.capacity if context_length is None else context_length
         self.actual_seq_lengths_kv = ([self.context_length] * positions.shape[0]
                                       if valid_length_kv else None)
-        self.plan = None  # the step's ranking of the requests (prepare), read by every layer
+        self.plan = None  # the step's plan of the requests (prepare), read by every layer
         self._plan = None
 
     def prepare(self):
         """Per-step hook, run after the positions change and before the layers (SlotGraph.compute
         does).  The reference rebuilds its scatter indices from the positions here
-        (continuous.py:147-150); the HIP writer reads the positions directly, and this ranks the
-        requests by length once for all the step's layers (``decode_plan``), so that no layer's
-        launch of the bundled decode grid ranks them itself.  The plan buffer is allocated on
-        the first call (SlotGraph's eager pass, before capture) and refilled by a kernel after."""
+        (continuous.py:147-150); the HIP writer reads the positions directly, and this cuts the
+        step's keys into the bundled grid's equal shares once for all the step's layers
+        (``decode_plan``).  The plan buffer is allocated on the first call (SlotGraph's eager
+        pass, before capture) and refilled by a kernel after."""
         positions = self.positions
         batch = positions.shape[0]
-        if not (positions.is_cuda and positions.ndim == 1 and positions.dtype == torch.int64
-                and 0 < batch <= PLAN_MAX_BATCH):
+        config = self.arena.reference.config
+        q_heads, kv_heads = config.num_attention_heads, config.num_key_value_heads
+        shape = plan_shape(batch, q_heads, kv_heads) if 0 < batch <= PLAN_MAX_BATCH else None
+        if not (positions.is_cuda and positions.ndim == 1 and positions.dtype == torch.int64 and shape):
             self.plan = None
             return
-        if self._plan is None or self._plan.shape[0] != batch or self._plan.device != positions.device:
-            self._plan = torch.empty(batch, 2, device=positions.device, dtype=torch.int32)
-        self.plan = decode_plan(positions, self.arena.capacity, out=self._plan)
+        if self._plan is None or tuple(self._plan.shape) != shape or self._plan.device != positions.device:
+            self._plan = torch.empty(shape, device=positions.device, dtype=torch.int32)
+        self.plan = decode_plan(positions, self.arena.capacity, q_heads, kv_heads, out=self._plan)
 
     def update(self, keys, values, layer_idx, cache_kwargs):
         batch = keys.shape[0]

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol(pkg):
 
 def test_status_strings_and_version(pkg):
     lib = pkg.library()
-    assert lib.q3t_abi_version() == 6
+    assert lib.q3t_abi_version() == 7
     assert lib.q3t_status_string(0) == b"success"
     assert lib.q3t_status_string(-1) == b"invalid argument"
     assert lib.q3t_status_string(-3) == b"workspace missing or too small"
@@ -81,11 +81,22 @@ def test_rejected_calls_return_negative_status_without_a_gpu(pkg):
     assert lib.q3t_decode_attention(args, None) == -2   # two query tokens: not on the bundled grid
     args.grid, args.query_len = 0, 1
     assert lib.q3t_decode_reset_workspace(None, 1 << 20, None) == -3
-    assert lib.q3t_decode_plan(None, 4, 1024, 16, None) == -1      # no positions
-    assert lib.q3t_decode_plan(16, 129, 1024, 16, None) == -1      # more requests than a plan ranks
-    assert lib.q3t_decode_plan(16, 4, 0, 16, None) == -1           # no arena rows
-    assert lib.q3t_decode_plan(16, 4, (1 << 20) + 1, 16, None) == -1
-    assert lib.q3t_decode_plan(None, 0, 1024, None, None) == 0     # an empty batch launches nothing
+    assert lib.q3t_decode_plan(None, 4, 1024, 16, 8, 16, None) == -1      # no positions
+    assert lib.q3t_decode_plan(16, 129, 1024, 16, 8, 16, None) == -1      # more requests than a plan covers
+    assert lib.q3t_decode_plan(16, 4, 0, 16, 8, 16, None) == -1           # no arena rows
+    assert lib.q3t_decode_plan(16, 4, (1 << 20) + 1, 16, 8, 16, None) == -1
+    assert lib.q3t_decode_plan(16, 4, 1024, 24, 8, 16, None) == -1        # 3 query heads per KV head
+    assert lib.q3t_decode_plan(16, 4, 1024, 16, 8, 8, None) == -1         # plan not 16-byte aligned
+    assert lib.q3t_decode_plan(None, 0, 1024, 16, 8, None, None) == 0     # an empty batch launches nothing
+    # the plan's size: 32 shares per KV head of 8 (one workgroup per CU) and a header row,
+    # 8 entries of 16 bytes each (more shares when a batch needs more than 4 requests per
+    # share), then the ranking section: (batch, 0) and 128 (b, L) pairs of 4-byte ints
+    ranking = (2 + 2 * 128) * 4
+    assert lib.q3t_decode_plan_bytes(64, 16, 8) == 33 * 8 * 16 + ranking
+    assert lib.q3t_decode_plan_bytes(128, 16, 16) == 33 * 8 * 16 + ranking
+    assert lib.q3t_decode_plan_bytes(128, 64, 64) == 33 * 8 * 16 + ranking
+    assert lib.q3t_decode_plan_bytes(128, 4, 4) == 65 * 8 * 16 + ranking
+    assert lib.q3t_decode_plan_bytes(64, 24, 8) == -1
     # the allocation-free entry point refuses, before touching any device, a call whose split
     # states would not fit its fixed 8 MiB array (1024 requests x 8 heads x 16 chunks)
     big = pkg._lib.DecodeArgs()
@@ -140,8 +151,9 @@ def test_decode_workspace_sizes(pkg):
 
 def test_decode_grid_choice(pkg):
     """The library's grid choice, without a GPU: the talker step (64 requests, 1024-row arena)
-    runs bundled, long arenas balanced, short ones and small batches chunked; splits still
-    selects balanced (> 0) or chunked (< 0) under the automatic choice."""
+    runs bundled, also with the reference's mask when it brings the step's plan, long arenas
+    balanced, short ones and small batches chunked; splits still selects balanced (> 0) or
+    chunked (< 0) under the automatic choice."""
     decode_grid_for = pkg.decode_grid_for
     assert decode_grid_for(64, 1, 16, 8, 128, 1024) == "bundled"
     assert decode_grid_for(128, 1, 16, 8, 128, 1500) == "bundled"
@@ -149,7 +161,8 @@ def test_decode_grid_choice(pkg):
     assert decode_grid_for(64, 1, 16, 8, 128, 16) == "chunked"
     assert decode_grid_for(32, 1, 16, 8, 128, 1024) == "chunked"
     assert decode_grid_for(64, 2, 16, 8, 128, 1024) == "chunked"
-    assert decode_grid_for(64, 1, 16, 8, 128, 1024, masked=True) == "chunked"
+    assert decode_grid_for(64, 1, 16, 8, 128, 1024, masked=True) == "bundled"
+    assert decode_grid_for(64, 1, 16, 8, 128, 1024, masked=True, planned=False) == "chunked"
     assert decode_grid_for(64, 1, 16, 8, 128, 1024, torch.float32) == "chunked"
     assert decode_grid_for(64, 1, 16, 8, 128, 1024, splits=-1) == "chunked"
     assert decode_grid_for(64, 1, 16, 8, 128, 1024, splits=9) == "balanced"

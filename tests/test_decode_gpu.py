@@ -12,7 +12,7 @@ from oracle import attention as oatt
 from oracle import bf16 as obf16
 from oracle import kv as okv
 from oracle import rope as orope
-from tests._util import assert_attention_close, bits, f64
+from tests._util import assert_attention_close, bits, f64, from_bits
 
 pytestmark = pytest.mark.gpu
 
@@ -144,64 +144,184 @@ def test_bundled_grid_edges(pkg, device, group, batch, capacity, fused):
     idx = np.flatnonzero(valid.numpy())
     expected = oatt.decode_attention(query[idx], keys[idx], values[idx], contexts.numpy()[idx], D ** -0.5)
     assert_attention_close(got[idx], expected)
-    # the same launch from the step's plan: the same bundles, so the same bits
-    plan = pkg.decode_plan(positions, capacity)
+    # the same launch from the step's plan: its ranking is the one the launch makes itself,
+    # so the outputs are bit-identical; and masked by SlotGraph.compute's mask (0 up to each
+    # position, the most negative bf16 after), the plan's equal shares of each head's keys
+    # (requests cut between shares merged through the workspace): the same arena rows,
+    # outputs in the bar
+    plan = pkg.decode_plan(positions, capacity, q_heads, kv_heads)
+    allowed = torch.arange(capacity, device=device)[None, :] <= positions[:, None]
+    mask = torch.where(allowed, 0.0, torch.finfo(torch.bfloat16).min).to(torch.bfloat16)[:, None, None, :]
     if fused:
-        k2, v2 = torch.from_numpy(before_k.view(np.int16)).view(torch.bfloat16).to(device), \
-            torch.from_numpy(before_v.view(np.int16)).view(torch.bfloat16).to(device)
+        k2, v2 = from_bits(before_k, device), from_bits(before_v, device)
         planned = pkg.decode_step(q, kn, vn, k2, v2, positions, cos, sin, grid="bundled", plan=plan)
         assert np.array_equal(bits(k2), bits(k)) and np.array_equal(bits(v2), bits(v))
+        k3, v3 = from_bits(before_k, device), from_bits(before_v, device)
+        masked = pkg.decode_step(q, kn, vn, k3, v3, positions, cos, sin, grid="bundled", plan=plan, mask=mask)
+        assert np.array_equal(bits(k3), bits(k)) and np.array_equal(bits(v3), bits(v))
     else:
         planned = pkg.decode_attention(q, k, v, positions, grid="bundled", plan=plan)
+        masked = pkg.decode_attention(q, k, v, positions, grid="bundled", plan=plan, mask=mask)
     assert torch.equal(planned, out)
+    got = f64(masked)
+    assert not got[~valid.numpy()].any()
+    assert_attention_close(got[idx], expected)
 
 
-def _plan_expected(contexts, capacity):
+SLOTS, LAST, MERGE, PUBLISH = 8, 1, 2, 4
+RANKS = 128
+
+
+def plan_parts(plan):
+    """Views of a plan tensor: the shares' segment entries (shares, 8, 4), the 32-int header
+    and the ranking section (129, 2): (batch, 0), then (b, L) of each rank."""
+    shares = (plan.numel() - 2 - 2 * RANKS) // (SLOTS * 4) - 1
+    entries = plan[:shares * SLOTS * 4].view(shares, SLOTS, 4)
+    header = plan[shares * SLOTS * 4:(shares + 1) * SLOTS * 4]
+    ranking = plan[(shares + 1) * SLOTS * 4:].view(RANKS + 1, 2)
+    return entries, header, ranking
+
+
+def check_plan(plan, contexts, capacity, q_heads, kv_heads):
+    """The plan's contract: a header (batch, shares, segment cap, capacity, zero-length mask);
+    every key of every request in exactly one segment; entries a prefix of each share's 8
+    slots, at most 16 / group of them; a request cut between shares has its earlier parts in
+    the first slot of the shares before (published) and its last part in the last slot of its
+    final share (merging them); and, unless it fell back to whole requests, shares of whole
+    64-key stages within one stage of each other, the last one excepted.  The ranking section
+    lists every request once, by length descending with ties by index, (-1, 0) past the batch.
+    Returns (fell back, stages per share)."""
+    entries, header, ranking = (t.cpu().numpy() for t in plan_parts(plan))
+    e = entries
+    shares = e.shape[0]
+    batch = len(contexts)
     lengths = np.where((contexts >= 0) & (contexts < capacity), contexts + 1, 0)
-    order = np.lexsort((np.arange(len(contexts)), -lengths))  # longest first, ties by index
-    return np.stack([order, lengths[order]], 1).astype(np.int32)
+    cap = min(SLOTS, 16 // (q_heads // kv_heads))
+    assert list(header[:4]) == [batch, shares, cap, capacity] and not header[8:].any()
+    zero = sum(1 << b for b in range(batch) if lengths[b] == 0)
+    assert sum(int(np.uint32(header[4 + w])) << (32 * w) for w in range(4)) == zero
+    order = sorted(range(batch), key=lambda b: (-lengths[b], b))
+    assert list(ranking[0]) == [batch, 0]
+    assert [tuple(r) for r in ranking[1:batch + 1]] == [(b, lengths[b]) for b in order]
+    assert (ranking[batch + 1:] == [-1, 0]).all()
+    covered = [np.zeros(n, int) for n in lengths]
+    keys, whole = [], True
+    for m in range(shares):
+        slots = e[m]
+        live = slots[:, 0] >= 0
+        n = int(live.sum())
+        assert live[:n].all() and n <= cap
+        total = 0
+        for k in range(n):
+            b, j0, j1, info = slots[k]
+            assert 0 <= b < batch and 0 <= j0 < j1 <= lengths[b]
+            covered[b][j0:j1] += 1
+            total += j1 - j0
+            assert bool(info & LAST) == (j1 == lengths[b])
+            whole = whole and j0 == 0 and j1 == lengths[b]
+            assert bool(info & PUBLISH) == (j1 < lengths[b])
+            if info & PUBLISH:
+                assert k == 0
+            assert bool(info & MERGE) == (j0 > 0 and j1 == lengths[b])
+            if info & MERGE:
+                assert k == n - 1
+                for i in range(1, (info >> 4) + 1):
+                    assert e[m - i][0][0] == b and e[m - i][0][3] & PUBLISH
+        keys.append(total)
+    assert all((c == 1).all() for c in covered)
+    stages = [(n + 63) // 64 for n in keys]
+    if not whole:
+        body = stages[:-1]
+        assert max(body) - min(body) <= 1 and stages[-1] <= max(body)
+    return whole, stages
 
 
-@pytest.mark.parametrize("batch", [1, 6, 64, 100, 128])
-def test_decode_plan_ranks_longest_first(pkg, device, batch):
-    """The step's ranking against a stable numpy sort: ties (repeated lengths) by request
-    index, invalid positions (negative, at or past the capacity) ranked last with 0 keys."""
-    capacity = 1024
+@pytest.mark.parametrize("batch,capacity,group", [(1, 1024, 2), (6, 1024, 2), (64, 1024, 2), (100, 2048, 1),
+                                                  (128, 1024, 4), (16, 4096, 2)])
+def test_decode_plan_cuts_equal_shares(pkg, device, batch, capacity, group):
+    """The step's plan on the device: ties, invalid positions (negative, at or past the
+    capacity: no keys, listed in the header's mask) and, for 16 requests over 4096 rows,
+    requests spanning more than three shares (whole requests instead)."""
     gen = torch.Generator().manual_seed(900 + batch)
     contexts = torch.randint(-2, capacity + 2, (batch,), generator=gen)
-    contexts[: batch // 3] = contexts[0]  # ties
-    plan = pkg.decode_plan(contexts.to(device), capacity)
-    assert plan.shape == (batch, 2) and plan.dtype == torch.int32
-    np.testing.assert_array_equal(plan.cpu().numpy(), _plan_expected(contexts.numpy(), capacity))
+    contexts[: batch // 3] = contexts[0]
+    kv_heads = 8 if group < 4 else 4
+    plan = pkg.decode_plan(contexts.to(device), capacity, kv_heads * group, kv_heads)
+    assert tuple(plan.shape) == pkg.plan_shape(batch, kv_heads * group, kv_heads) and plan.dtype == torch.int32
+    check_plan(plan, contexts.numpy(), capacity, kv_heads * group, kv_heads)
     with pytest.raises(ValueError):
-        pkg.decode_plan(torch.zeros(129, dtype=torch.int64, device=device), capacity)
+        pkg.decode_plan(torch.zeros(129, dtype=torch.int64, device=device), capacity, 16, 8)
+    with pytest.raises(ValueError):
+        pkg.decode_plan(contexts.to(device), capacity, 24, 8)
 
 
-def test_decode_plan_of_other_positions_stays_in_bounds(pkg, device):
-    """A plan is only valid for the positions it was made from.  A stale or malformed one
-    (request indices outside the batch, lengths past the arena) gives other outputs but
-    touches nothing outside the arguments: entries naming no request are skipped, lengths are
-    clamped to the arena, and the output rows of requests it does not name stay as they were."""
+def test_decode_plan_of_the_talker_step(pkg, device):
+    """The headline step's plan: 32 shares per head, all of 16 stages but one of 17 (the
+    seed-0 draw has 32,782 keys per head, 513 stages), no fallback."""
+    contexts, *_ = _config2(device)
+    plan = pkg.decode_plan(contexts.to(device), 1024, HQ, HKV)
+    whole, stages = check_plan(plan, contexts.numpy(), 1024, HQ, HKV)
+    assert not whole and sorted(stages) == [16] * 31 + [17]
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_decode_plan_of_other_positions_stays_in_bounds(pkg, device, masked):
+    """A plan is only valid for the positions it was made from.  A stale one (made for other
+    positions) or a malformed one (entries naming no request, key ranges past the arena)
+    gives other outputs but touches nothing outside the arguments: the fused step writes the
+    new K/V rows at the rows the plan names (the last key of each request it lists) and
+    nowhere else, and the output rows of requests it does not name stay as they were.  A plan
+    of another batch gives NaN rows masked; unmasked it is not used (the launch ranks the
+    requests itself)."""
     contexts, k, v, q, kn, vn = _config2(device, seed=13)
     positions = contexts.to(device)
     cos, sin = pkg.rope_tables(positions, D)
-    bad = pkg.decode_plan(positions, 1024).clone()
-    bad[::3, 0] = 1000      # no such request
-    bad[1::3, 1] = 5000     # more keys than the arena has
-    out = torch.full((64, 1, HQ, D), 7.0, device=device, dtype=torch.bfloat16)
-    pkg.decode_attention(q, k, v, positions, grid="bundled", plan=bad, out=out)
+    mask = None
+    if masked:  # keys up to 1023 allowed: the positions and the plan's lengths decide
+        mask = torch.zeros(64, 1, 1, 1024, device=device, dtype=torch.bfloat16)
+    gen = torch.Generator().manual_seed(14)
+    stale_ctx = torch.randint(64, 1025, (64,), generator=gen)
+    stale = pkg.decode_plan(stale_ctx.to(device), 1024, HQ, HKV)
+    before_k, before_v = bits(k).copy(), bits(v).copy()
+    pkg.decode_step(q, kn, vn, k, v, positions, cos, sin, grid="bundled", plan=stale, mask=mask)
     torch.cuda.synchronize()
-    named = set(bad[:, 0].cpu().tolist())
+    changed = np.argwhere((bits(k) != before_k).any(-1) | (bits(v) != before_v).any(-1))
+    allowed = {(b, h, int(stale_ctx[b])) for b in range(64) for h in range(HKV)}
+    assert changed.shape[0] > 0 and {tuple(int(x) for x in r) for r in changed} <= allowed
+    bad = stale.clone()
+    entries, _, ranking = plan_parts(bad)
+    if masked:
+        entries[::3, 0, 0] = 1000     # no such request: the share lists nothing
+        entries[1::3, 0, 2] = 5000    # more keys than the arena has: clamped
+        named = set(int(b) for b in entries[:, :, 0].reshape(-1).cpu().tolist() if 0 <= b < 64)
+    else:
+        ranking[1::3, 0] = 1000       # no such request: the rank attends nothing
+        ranking[2::3, 1] = 5000       # more keys than the arena has: clamped
+        named = set(int(b) for b in ranking[1:65, 0].cpu().tolist() if 0 <= b < 64)
+    out = torch.full((64, 1, HQ, D), 7.0, device=device, dtype=torch.bfloat16)
+    pkg.decode_attention(q, k, v, positions, grid="bundled", plan=bad, out=out, mask=mask)
+    torch.cuda.synchronize()
+    assert masked or len(named) < 64
     for b in range(64):
         if b not in named:
             assert torch.all(out[b] == 7.0)
+    # a plan edited by hand can list a request's later part without its first one, whose
+    # share would have consumed the later part's published state: re-zero the workspace
+    pkg.reset_workspaces(device)
+    other = pkg.decode_plan(positions[:60], 1024, HQ, HKV)  # 60 requests: the same plan shape
+    out = pkg.decode_attention(q, k, v, positions, grid="bundled", plan=other, mask=mask)
+    if masked:
+        assert torch.isnan(out.float()).all()
+    else:
+        assert torch.equal(out, pkg.decode_attention(q, k, v, positions, grid="bundled"))
     with pytest.raises(ValueError):
-        pkg.decode_attention(q, k, v, positions, grid="bundled", plan=bad[:10])
+        pkg.decode_attention(q, k, v, positions, grid="bundled", plan=stale[:10], mask=mask)
 
 
 def test_bundled_grid_is_deterministic_and_refuses_what_it_cannot_run(pkg, device):
-    """Repeated launches are bit-identical; asked for by name, the grid refuses a mask, two
-    query tokens and fp32 rows (the automatic choice runs them on another grid)."""
+    """Repeated launches are bit-identical, with and without the step's plan; asked for by
+    name, the grid refuses a mask without a plan, two query tokens and fp32 rows (the
+    automatic choice runs them on another grid)."""
     contexts, k, v, q, _, _ = _config2(device, seed=12)
     positions = contexts.to(device)
     first = pkg.decode_attention(q, k, v, positions, grid="bundled").clone()
@@ -209,6 +329,13 @@ def test_bundled_grid_is_deterministic_and_refuses_what_it_cannot_run(pkg, devic
         assert torch.equal(pkg.decode_attention(q, k, v, positions, grid="bundled"), first)
     expected = oatt.decode_attention(f64(q), f64(k), f64(v), contexts.numpy(), D ** -0.5)
     assert_attention_close(f64(first), expected)
+    plan = pkg.decode_plan(positions, 1024, HQ, HKV)
+    assert torch.equal(pkg.decode_attention(q, k, v, positions, grid="bundled", plan=plan), first)
+    mask = torch.zeros(64, 1, 1, 1024, device=device, dtype=torch.bfloat16)
+    planned = pkg.decode_attention(q, k, v, positions, grid="bundled", plan=plan, mask=mask).clone()
+    for _ in range(10):
+        assert torch.equal(pkg.decode_attention(q, k, v, positions, grid="bundled", plan=plan, mask=mask), planned)
+    assert_attention_close(f64(planned), expected)
     keep = torch.arange(1024, device=device)[None, None, None, :] <= positions[:, None, None, None]
     with pytest.raises(ValueError, match="unsupported"):
         pkg.decode_attention(q, k, v, positions, mask=keep, grid="bundled")
