@@ -541,6 +541,31 @@ def main():
     torch.cuda.synchronize()
     attn_us = start.elapsed_time(stop) * 1e3 / (reps * LAYERS)
 
+    # the reference's own flow: SlotGraph.compute hands every layer the (B, 1, 1, ctx) additive
+    # mask j <= pos[b] (continuous.py:188-197), a masked launch (the shares kernel)
+    allowed = torch.arange(CAPACITY, device=device)[None, :] <= positions[:, None]
+    ref_mask = torch.where(allowed, 0.0, torch.finfo(torch.bfloat16).min).to(torch.bfloat16)[:, None, None, :]
+    masked_graph = torch.cuda.CUDAGraph()
+
+    def masked_step():
+        plan = pkg.decode_plan(positions, CAPACITY, HQ, HKV, out=plan_buf)
+        for q, k, v, ak, av, o in views:
+            pkg.decode_step(q, k, v, ak, av, positions, cos, sin, out=o, mask=ref_mask, plan=plan)
+
+    masked_step()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(masked_graph):
+        masked_step()
+    masked_graph.replay()
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(reps):
+        masked_graph.replay()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    masked_us = start.elapsed_time(stop) * 1e3 / (reps * LAYERS)
+    masked_grid = pkg.decode_grid_for(BATCH, 1, HQ, HKV, D, CAPACITY, masked=True)
+
     calibration_copy(pkg, device, args.calibrate_bytes, stream)
 
     extra = {}
@@ -581,6 +606,12 @@ def main():
                    "us_per_layer_attention_only": attn_us,
                    "attention_only_GBs": attention_bytes(contexts) / (attn_us * 1e-6) / 1e9,
                    "decode_plan": not args.no_plan,
+                   "reference_masked_step": {
+                       "workload": "the same step with SlotGraph.compute's (64, 1, 1, 1024) bf16 mask "
+                                   "handed to every layer (the reference's flow), with the step's plan",
+                       "grid": masked_grid,
+                       "us_per_layer_launch": masked_us,
+                       "tokens_per_s": BATCH / (masked_us * LAYERS * 1e-6)},
                    "max_chunks": args.max_chunks,
                    "splits": args.splits,
                    "wall_s_timed_region": wall,

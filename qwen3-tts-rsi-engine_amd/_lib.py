@@ -158,6 +158,26 @@ def stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+_HIP = None
+
+
+def capture_id(stream: int) -> int:
+    """Id of the graph capture ``stream`` is recording into (hipStreamGetCaptureInfo), 0 when
+    it is not capturing."""
+    global _HIP
+    if _HIP is None:
+        hip = ctypes.CDLL('libamdhip64.so')  # the HIP runtime torch has loaded
+        hip.hipStreamGetCaptureInfo.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int),
+                                                ctypes.POINTER(ctypes.c_ulonglong)]
+        hip.hipStreamGetCaptureInfo.restype = ctypes.c_int
+        _HIP = hip
+    status, cid = ctypes.c_int(0), ctypes.c_ulonglong(0)
+    err = _HIP.hipStreamGetCaptureInfo(ctypes.c_void_p(stream), ctypes.byref(status), ctypes.byref(cid))
+    if err != 0:
+        raise KernelError(f'hipStreamGetCaptureInfo failed: error {err}')
+    return int(cid.value) if status.value == 1 else 0  # hipStreamCaptureStatusActive
+
+
 def require_gpu(*tensors: torch.Tensor) -> torch.device:
     """All tensors on one ROCm device; the HIP kernels are the only implementation."""
     device = tensors[0].device

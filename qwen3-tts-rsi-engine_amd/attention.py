@@ -20,38 +20,32 @@ _WORKSPACES: dict = {}
 _RETIRED: list = []
 
 
-class _Workspace:
-    __slots__ = ('buffer', 'captured')
-
-    def __init__(self, buffer):
-        self.buffer = buffer
-        self.captured = False  # a graph captured a launch that uses this buffer
-
-
 def workspace(device: torch.device, nbytes: int, stream: int | None = None) -> torch.Tensor:
-    """Split-softmax workspace of one stream of ``device``, its counters zeroed.
+    """Split-softmax workspace of one stream of ``device``, or of one graph capture, its
+    counters zeroed.
 
     Kernels leave the counters zeroed, so one buffer serves every sequential launch on its
-    stream; launches on different streams get different buffers, so they may overlap.  A
-    new buffer's counters are cleared by the library's reset kernel on that stream, which
-    is a kernel node when the stream is being captured (no memset node in a graph), so a
-    buffer can also be created during capture; it then comes from the graph's memory pool.
-    A replaced buffer that some captured graph uses stays alive with the process (the graph
-    may be replayed); one that no graph captured is released at once."""
+    stream; launches on different streams get different buffers, so they may overlap.  Eager
+    launches share the stream's buffer, zeroed by the library's reset kernel when it is
+    created.  A launch being captured gets the buffer of its capture instead (keyed by the
+    capture id), created in the graph's memory pool and zeroed by a reset kernel recorded in
+    that graph ahead of its first use, so every replay starts from zeroed counters and no two
+    graphs share a buffer (they may be replayed in any order, also on different streams; one
+    graph's replays must not overlap each other).  A buffer that grows during a capture keeps
+    the old one alive with the process (the graph's earlier launches use it); an eager buffer
+    replaced by a larger one is released at once."""
     stream = _lib.stream_handle(device) if stream is None else stream
-    key = (device, stream)
     capturing = torch.cuda.is_current_stream_capturing()
+    key = (device, stream, _lib.capture_id(stream) if capturing else 0)
     current = _WORKSPACES.get(key)
-    if current is None or current.buffer.numel() < nbytes:
+    if current is None or current.numel() < nbytes:
         buffer = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         status = _lib.library().q3t_decode_reset_workspace(buffer.data_ptr(), buffer.numel(), stream)
         _lib.check(status, 'decode workspace')
-        if current is not None and current.captured:
-            _RETIRED.append(current.buffer)
-        _WORKSPACES[key] = current = _Workspace(buffer)
-    if capturing:
-        current.captured = True
-    return current.buffer
+        if current is not None and key[2]:
+            _RETIRED.append(current)
+        _WORKSPACES[key] = current = buffer
+    return current
 
 
 def reset_workspaces(device: torch.device | None = None) -> None:
@@ -59,11 +53,11 @@ def reset_workspaces(device: torch.device | None = None) -> None:
     on each workspace's own stream: after a launch that failed part-way, counters may be
     left non-zero and would mislead the next launch that splits a request."""
     lib = _lib.library()
-    for (dev, stream), ws in list(_WORKSPACES.items()):
+    for (dev, stream, _), ws in list(_WORKSPACES.items()):
         if device is not None and dev != torch.device(device):
             continue
         with torch.cuda.device(dev):
-            status = lib.q3t_decode_reset_workspace(ws.buffer.data_ptr(), ws.buffer.numel(), stream)
+            status = lib.q3t_decode_reset_workspace(ws.data_ptr(), ws.numel(), stream)
         _lib.check(status, 'decode workspace reset')
 
 
@@ -386,15 +380,19 @@ def _uniform_cu(batch, length, device):
 _LENGTH_POSITIONS: dict = {}
 
 
-def _length_positions(lengths, device):
-    """Device positions n - 1 for a list of key counts, cached: captured graphs keep using
-    the same tensor, and no host copy happens during capture."""
-    key = (tuple(int(n) for n in lengths), device)
+def _length_positions(lengths, device, counts=False):
+    """Device positions n - 1 (int64), or with ``counts`` the key counts n (int32), for a list
+    of key counts, cached: captured graphs keep using the same tensor, and no host copy
+    happens during capture."""
+    key = (tuple(int(n) for n in lengths), device, counts)
     cached = _LENGTH_POSITIONS.get(key)
     if cached is None:
         if torch.cuda.is_current_stream_capturing():
             raise ValueError('actual_seq_lengths_kv must be seen once before graph capture')
-        cached = torch.tensor([n - 1 for n in key[0]], device=device, dtype=torch.int64)
+        if counts:
+            cached = torch.tensor(key[0], device=device, dtype=torch.int32)
+        else:
+            cached = torch.tensor([n - 1 for n in key[0]], device=device, dtype=torch.int64)
         _LENGTH_POSITIONS[key] = cached
     return cached
 
@@ -404,8 +402,9 @@ def attention(module, query, key, value, attention_mask, **kwargs):
     (B, Hkv, ctx, D) BNSD; returns ((B, S, Hq, D) contiguous, None).
 
     ``kv_positions`` (a device int64 (B,) tensor, as kept by SlotCache) limits request b to
-    keys 0 ... kv_positions[b]; ``actual_seq_lengths_kv`` (list of ints) limits it to that
-    many keys; the mask, if any, is applied on top, as the reference's operator does."""
+    keys 0 ... kv_positions[b] (one or two queries: decode); ``actual_seq_lengths_kv`` (list
+    of ints) limits it to that many keys at any query length; the mask, if any, is applied on
+    top, as the reference's operator does (npu_attention.py:16-25)."""
     if module.training or kwargs.get('dropout', 0.0) != 0.0:
         raise ValueError('Native GQA is inference-only')
     if getattr(module, 'sliding_window', None) is not None:
@@ -428,14 +427,32 @@ def attention(module, query, key, value, attention_mask, **kwargs):
     if qlen <= 2:
         out = decode_attention(query.transpose(1, 2), key, value, positions, scale=scale, mask=mask)
         return out, None
+    if kwargs.get('kv_positions') is not None:
+        raise ValueError('kv_positions bounds one or two queries per request; for more, pass '
+                         'actual_seq_lengths_kv or a mask')
     if mask is None and not getattr(module, 'is_causal', True):
         raise ValueError('non-causal prefill without a mask is not supported')
     # several queries per request on the MFMA kernel: without a mask, causal with request b's
-    # queries at positions 0 ... qlen-1; with one (PrefillGraph's key-valid and causal mask,
-    # prefill_graph.py:36-37, or any other) every key is scored and the mask decides
+    # queries at positions 0 ... qlen-1 (and keys below actual_seq_lengths_kv[b]); with one
+    # (PrefillGraph's key-valid and causal mask, prefill_graph.py:36-37, or any other) every
+    # key is scored and the mask decides, the key counts folded into it
+    kv_lens = None
+    if lengths is not None:
+        if len(lengths) != batch:
+            raise ValueError('actual_seq_lengths_kv needs one key count per request')
+        if mask is None:
+            kv_lens = _length_positions(lengths, device, counts=True)
+        else:
+            beyond = (torch.arange(ctx, device=device)[None, :]
+                      >= _length_positions(lengths, device, counts=True)[:, None])[:, None, None, :]
+            view = mask if mask.ndim == 4 else mask.view((1,) * (4 - mask.ndim) + tuple(mask.shape))
+            if view.dtype == torch.bool:
+                mask = view & ~beyond
+            else:
+                mask = view.masked_fill(beyond, torch.finfo(view.dtype).min)
     cu = _uniform_cu(batch, qlen, device)
     q = query.transpose(1, 2).reshape(batch * qlen, query.shape[1], head_dim)
-    out = prefill_attention(q, key, value, cu, qlen, scale=scale, mask=mask)
+    out = prefill_attention(q, key, value, cu, qlen, scale=scale, mask=mask, kv_lens=kv_lens)
     return out.view(batch, qlen, query.shape[1], head_dim), None
 
 

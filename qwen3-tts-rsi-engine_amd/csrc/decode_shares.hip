@@ -83,35 +83,35 @@ typedef int i32x8_t __attribute__((ext_vector_type(8)));
 // Global-to-LDS loads with the device-scope (sc1) policy, for states another workgroup wrote
 // in this launch; 16 bytes or 4 bytes per lane at lds_base + size * lane.
 Q3T_DEVICE void load_to_lds16_coherent(i32x4_t rsrc, uint32_t voffset, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen sc1 lds"
+    asm volatile("s_mov_b32 m0, %0\n\t" Q3T_VMEM_SGPR_WAIT "buffer_load_dwordx4 %1, %2, 0 offen sc1 lds"
                  :: "s"(lds_base), "v"(voffset), "s"(rsrc) : "memory", "m0");
 }
 Q3T_DEVICE void load_to_lds4_coherent(i32x4_t rsrc, uint32_t voffset, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen sc1 lds"
+    asm volatile("s_mov_b32 m0, %0\n\t" Q3T_VMEM_SGPR_WAIT "buffer_load_dword %1, %2, 0 offen sc1 lds"
                  :: "s"(lds_base), "v"(voffset), "s"(rsrc) : "memory", "m0");
 }
 Q3T_DEVICE void load_to_lds4(i32x4_t rsrc, uint32_t voffset, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+    asm volatile("s_mov_b32 m0, %0\n\t" Q3T_VMEM_SGPR_WAIT "buffer_load_dword %1, %2, 0 offen lds"
                  :: "s"(lds_base), "v"(voffset), "s"(rsrc) : "memory", "m0");
 }
 // Stores issued from inline assembly, so that the loop knows exactly how many memory
 // operations it has in flight besides the ring's loads (the wait for a stage may then leave
 // them outstanding, see wait_slack); lanes with an offset outside the resource store nothing.
 Q3T_DEVICE void store16_asm(i32x4_t rsrc, uint32_t voffset, U4 v) {
-    asm volatile("buffer_store_dwordx4 %0, %1, %2, 0 offen\n\ts_nop 1"
+    asm volatile(Q3T_VMEM_SGPR_WAIT "buffer_store_dwordx4 %0, %1, %2, 0 offen\n\ts_nop 1"
                  :: "v"(__builtin_bit_cast(i32x4_t, v)), "v"(voffset), "s"(rsrc) : "memory");
 }
 Q3T_DEVICE void store16_asm_coherent(i32x4_t rsrc, uint32_t voffset, U4 v) {
-    asm volatile("buffer_store_dwordx4 %0, %1, %2, 0 offen sc1\n\ts_nop 1"
+    asm volatile(Q3T_VMEM_SGPR_WAIT "buffer_store_dwordx4 %0, %1, %2, 0 offen sc1\n\ts_nop 1"
                  :: "v"(__builtin_bit_cast(i32x4_t, v)), "v"(voffset), "s"(rsrc) : "memory");
 }
 Q3T_DEVICE void store8_asm_coherent(i32x4_t rsrc, uint32_t voffset, float a, float b) {
     typedef int i32x2_t __attribute__((ext_vector_type(2)));
     const i32x2_t v = {__float_as_int(a), __float_as_int(b)};
-    asm volatile("buffer_store_dwordx2 %0, %1, %2, 0 offen sc1\n\ts_nop 1" :: "v"(v), "v"(voffset), "s"(rsrc) : "memory");
+    asm volatile(Q3T_VMEM_SGPR_WAIT "buffer_store_dwordx2 %0, %1, %2, 0 offen sc1\n\ts_nop 1" :: "v"(v), "v"(voffset), "s"(rsrc) : "memory");
 }
 Q3T_DEVICE void store4_asm_coherent(i32x4_t rsrc, uint32_t voffset, int v) {
-    asm volatile("buffer_store_dword %0, %1, %2, 0 offen sc1" :: "v"(v), "v"(voffset), "s"(rsrc) : "memory");
+    asm volatile(Q3T_VMEM_SGPR_WAIT "buffer_store_dword %0, %1, %2, 0 offen sc1" :: "v"(v), "v"(voffset), "s"(rsrc) : "memory");
 }
 // The wait for a stage when `extra` memory operations went out after the stage's loads (in
 // issue order: this stage, the extra operations, the next stage): vmcnt(B + extra) lets the

@@ -214,13 +214,20 @@ Q3T_DEVICE i32x4_t scalar_rsrc(const void *base, uint32_t bytes) {
 // lanes fill one contiguous 1 KiB run); offsets past the resource's range write zeros.  The
 // load is issued from inline assembly so that the compiler does not insert a wait for it in
 // front of unrelated LDS reads; completion is awaited explicitly with wait_loads.
+// Every memory instruction issued from inline assembly is preceded by five wait states
+// (Q3T_VMEM_SGPR_WAIT): a VMEM instruction reading an SGPR that a VALU instruction wrote
+// (v_readlane / v_readfirstlane, which is how the compiler reloads spilled or lane-derived
+// resource words) needs them, the compiler does not insert them in front of inline assembly,
+// and without them the instruction can read a stale resource word: a store then lands nowhere
+// (out of range) and a load fills LDS with zeros.  The s_mov to m0 counts as one of them.
+#define Q3T_VMEM_SGPR_WAIT "s_nop 4\n\t"
 Q3T_DEVICE void load_to_lds16(i32x4_t rsrc, uint32_t voffset, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+    asm volatile("s_mov_b32 m0, %0\n\t" Q3T_VMEM_SGPR_WAIT "buffer_load_dwordx4 %1, %2, 0 offen lds"
                  :: "s"(lds_base), "v"(voffset), "s"(rsrc) : "memory", "m0");
 }
 // The same with the non-temporal cache policy, for rows a launch reads once.
 Q3T_DEVICE void load_to_lds16_stream(i32x4_t rsrc, uint32_t voffset, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+    asm volatile("s_mov_b32 m0, %0\n\t" Q3T_VMEM_SGPR_WAIT "buffer_load_dwordx4 %1, %2, 0 offen nt lds"
                  :: "s"(lds_base), "v"(voffset), "s"(rsrc) : "memory", "m0");
 }
 // Touch every 64-byte line of the kernel's argument segment (BYTES long) at once, so that the

@@ -17,6 +17,18 @@ from .attention import PLAN_MAX_BATCH, decode_plan, plan_shape
 from .packed_kv import copy_packed_prefix, copy_rows
 
 
+def _attention_heads(reference):
+    """(query heads, KV heads) of the talker's attention: the config's counts, or the first
+    layer's query projection over head_dim where the config names no query-head count."""
+    config = reference.config
+    q_heads = getattr(config, 'num_attention_heads', None)
+    if q_heads is None:
+        attn = reference.layers[0].self_attn
+        attn = getattr(attn, 'reference', attn)  # PackedAttention keeps the wrapped module
+        q_heads = attn.q_proj.out_features // config.head_dim
+    return q_heads, config.num_key_value_heads
+
+
 class SlotArena:
     """Per-slot KV storage for every talker layer.
 
@@ -133,8 +145,7 @@ class SlotCache(Cache):
         pass, before capture) and refilled by a kernel after."""
         positions = self.positions
         batch = positions.shape[0]
-        config = self.arena.reference.config
-        q_heads, kv_heads = config.num_attention_heads, config.num_key_value_heads
+        q_heads, kv_heads = _attention_heads(self.arena.reference)
         shape = plan_shape(batch, q_heads, kv_heads) if 0 < batch <= PLAN_MAX_BATCH else None
         if not (positions.is_cuda and positions.ndim == 1 and positions.dtype == torch.int64 and shape):
             self.plan = None

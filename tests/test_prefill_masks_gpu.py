@@ -117,6 +117,35 @@ def test_attention_dropin_takes_the_prefill_mask(pkg, device):
     assert_attention_close(f64(out), expected)
 
 
+@pytest.mark.parametrize("with_mask", [False, True])
+def test_attention_dropin_key_counts_at_any_query_length(pkg, device, with_mask):
+    """The reference operator takes actual_seq_lengths_kv at every query length
+    (npu_attention.py:20-24): with several queries the key counts bound every row, alone (the
+    causal rule) or on top of a causal mask, which gives the padded batch's key-valid and
+    causal mask (prefill_graph.py:36-37).  kv_positions, a decode bound, is refused there."""
+    class Module:
+        training, sliding_window, is_causal = False, None, True
+
+    lengths, padded = [64, 33, 64, 5], 64
+    batch = len(lengths)
+    gen = torch.Generator(device=device).manual_seed(9)
+    q = torch.randn(batch, padded, HQ, D, generator=gen, device=device, dtype=torch.bfloat16)
+    k = torch.randn(batch, padded, HKV, D, generator=gen, device=device, dtype=torch.bfloat16)
+    v = torch.randn_like(k)
+    mask = None
+    if with_mask:  # causal only: the key counts come from actual_seq_lengths_kv
+        mask = _padded_mask([padded] * batch, padded, torch.bfloat16).to(device)
+    out, _ = pkg.attention(Module(), q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), mask,
+                           scaling=D ** -0.5, actual_seq_lengths_kv=lengths)
+    expected = oatt.decode_attention(f64(q), f64(k.transpose(1, 2)), f64(v.transpose(1, 2)),
+                                     np.full(batch, padded - 1), D ** -0.5,
+                                     mask=_padded_mask(lengths, padded, torch.bool)[:, 0].numpy())
+    assert_attention_close(f64(out), expected)
+    with pytest.raises(ValueError):
+        pkg.attention(Module(), q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), mask,
+                      kv_positions=torch.full((batch,), padded - 1, device=device))
+
+
 # ---- the PrefillGraph flow on a stand-in talker --------------------------------------------
 
 class _TalkerWithHead(torch.nn.Module):

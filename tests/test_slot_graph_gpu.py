@@ -24,6 +24,7 @@ from oracle import kv as okv
 from oracle import rope as orope
 from tests._talker import Talker
 from tests._util import bits
+from tests.test_decode_gpu import plan_parts
 
 pytestmark = pytest.mark.gpu
 
@@ -113,8 +114,17 @@ def _cpu_step(talker, arena, inputs, positions, rotary):
     return talker.norm(x)
 
 
-def test_graph_step_matches_the_oracle(pkg, device):
-    slots, capacity, batch, layers, hidden = 16, 256, 12, 3, 512
+@pytest.mark.parametrize("shape", ["small", "talker", "talker_reference_mask"])
+def test_graph_step_matches_the_oracle(pkg, device, shape):
+    """small: 12 requests over 16 slots of a 256-row arena, 3 layers (the chunked grid).
+    talker: 64 slots of a 1024-row arena, 2 layers (the bundled grid, each step's plan made by
+    SlotCache.prepare).  talker_reference_mask: the same step as the reference's
+    SlotGraph.compute runs it, the (B, 1, 1, ctx) 0 / finfo.min mask built every step and
+    handed to every layer (continuous.py:188-197): the masked bundled launch."""
+    slots, capacity, batch, layers, counts = {"small": (16, 256, 12, 3, [12, 9]),
+                                              "talker": (64, 1024, 64, 2, [64, 40]),
+                                              "talker_reference_mask": (64, 1024, 64, 2, [64, 40])}[shape]
+    hidden = 512
     model = _model(pkg, device, layers=layers, hidden=hidden)
     cpu_talker = Talker(layers=layers, hidden=hidden, seed=3).eval()
     arena = _arena(pkg, model, slots, capacity, 14)
@@ -122,10 +132,15 @@ def test_graph_step_matches_the_oracle(pkg, device):
     twin_arena = pkg.SlotArena(model, slots, capacity, packed_kv=True)
     graph = pkg.SlotGraph(arena, batch)
     assert graph._mask(torch.bfloat16) is None                 # every layer is wrapped
+    reference_mask = shape == "talker_reference_mask"
+    if shape != "small":
+        assert pkg.decode_grid_for(batch, 1, 16, 8, 128, capacity, masked=reference_mask) == 'bundled'
+    graph._needs_mask = reference_mask
     graph.capture()
     twin = pkg.SlotGraph(twin_arena, batch)
+    twin._needs_mask = reference_mask
     gen = torch.Generator().manual_seed(15)
-    for step, count in enumerate([12, 9]):
+    for step, count in enumerate(counts):
         positions = torch.zeros(batch, dtype=torch.long)
         positions[:count] = torch.randint(1, capacity, (count,), generator=gen)
         inputs = torch.randn(batch, 1, hidden, generator=gen).bfloat16()
@@ -160,7 +175,10 @@ def test_graph_step_matches_the_oracle(pkg, device):
         assert np.array_equal(bits(arena.packed), expected_arena), f"step {step}"
         expected = _cpu_step(cpu_talker, mirror, inputs, positions.numpy(), rotary)
         err = (out.float().cpu() - expected.float()).abs()
-        assert err.max().item() <= 3e-2 and err.mean().item() <= 3e-3, (step, err.max().item(), err.mean().item())
+        # 3e-2 absolute, widened by half a bf16 step of the value (one step is 2^-5 = 0.031 at
+        # magnitudes 4-8, where GEMM accumulation order alone moves an output by one step)
+        bound = 3e-2 + expected.float().abs() * 2.0 ** -8
+        assert bool((err <= bound).all()) and err.mean().item() <= 3e-3, (step, err.max().item(), err.mean().item())
         mirror = bits(arena.packed).copy()                    # next step starts from the device arena
     graph.close()
 
@@ -179,9 +197,9 @@ def test_mask_is_built_only_for_unwrapped_layers(pkg, device):
 
 def test_talker_step_on_the_bundled_grid_reads_the_step_plan(pkg, device):
     """At the talker's shape (64 slots of a 1024-row arena, 8 KV heads of 128: the bundled
-    grid) SlotCache.prepare ranks the step's requests once (decode_plan) and every layer's
-    launch reads that ranking: replays equal an eager twin whose cache holds no plan (each
-    launch ranks the requests itself), output and arena bit-identical, and the plan equals a
+    grid) SlotCache.prepare plans the step once (decode_plan) and every layer's launch reads
+    the plan's ranking: replays equal an eager twin whose cache holds no plan (each launch
+    ranks the requests itself), output and arena bit-identical, and the ranking equals a
     stable sort by length."""
     slots, capacity, batch = 64, 1024, 64
     model = _model(pkg, device, layers=2)
@@ -209,7 +227,8 @@ def test_talker_step_on_the_bundled_grid_reads_the_step_plan(pkg, device):
         assert twin.cache.plan is None and graph.cache.plan is not None
         lengths = positions.numpy() + 1
         order = np.lexsort((np.arange(batch), -lengths))
-        np.testing.assert_array_equal(graph.cache.plan.cpu().numpy(), np.stack([order, lengths[order]], 1))
+        ranking = plan_parts(graph.cache.plan)[2].cpu().numpy()
+        np.testing.assert_array_equal(ranking[1:batch + 1], np.stack([order, lengths[order]], 1))
         assert np.array_equal(bits(out), bits(expected)), f"step {step}"
         assert np.array_equal(bits(arena.packed), bits(twin_arena.packed)), f"step {step}"
     graph.close()

@@ -62,3 +62,36 @@ def test_no_alloc_rejects_calls_beyond_its_array(pkg, device):
         pkg.decode_attention(q, keys, keys, positions, splits=-1, max_chunks=16, out=out, no_alloc=True)
     torch.cuda.synchronize()
     assert bool((out == 7.0).all())
+
+
+@pytest.mark.parametrize("grid", [(-1, 4), (24, 0)])
+def test_no_alloc_entry_point_under_graph_capture(pkg, device, grid):
+    """Recorded in a graph (the callers the entry point is for) and replayed with the
+    positions, the step's rows and the arena rewritten in place: every replay matches the
+    workspace entry point run eagerly on the same inputs, bit for bit."""
+    splits, max_chunks = grid
+    keys, values, qkv, positions = _inputs(64, 1024, 92, device)
+    q, k, v = _split(qkv, 64)
+    cos, sin = pkg.rope_tables(positions, D)
+    out = torch.empty(64, 1, HQ, D, device=device, dtype=torch.bfloat16)
+    pkg.decode_step(q, k, v, keys, values, positions, cos, sin, splits=splits, max_chunks=max_chunks,
+                    no_alloc=True, out=out)  # eager first call: the array's set-up
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.inference_mode(), torch.cuda.graph(graph):  # as the package's graphs are captured
+        pkg.decode_step(q, k, v, keys, values, positions, cos, sin, splits=splits, max_chunks=max_chunks,
+                        no_alloc=True, out=out)
+    gen = torch.Generator(device=device).manual_seed(93)
+    for _ in range(3):
+        positions.copy_(torch.randint(0, 1024, (64,), generator=gen, device=device))
+        qkv.copy_(torch.randn(qkv.shape, generator=gen, device=device, dtype=torch.bfloat16))
+        keys.copy_(torch.randn(keys.shape, generator=gen, device=device, dtype=torch.bfloat16))
+        c, s = pkg.rope_tables(positions, D)
+        cos.copy_(c)
+        sin.copy_(s)
+        k2, v2 = keys.clone(), values.clone()
+        expected = pkg.decode_step(q, k, v, k2, v2, positions, cos, sin, splits=splits, max_chunks=max_chunks)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, expected)
+        assert torch.equal(keys, k2) and torch.equal(values, v2)
