@@ -205,7 +205,7 @@ typedef struct q3t_decode_args {
        `positions`, `batch`, `ctx`, `q_heads` and `kv_heads` (device, q3t_decode_plan_bytes).
        A masked launch streams the plan's equal shares of each KV head's keys (requests cut
        between shares are merged through the workspace); an unmasked one takes whole requests
-       in the plan's ranking instead of ranking them itself.  A plan made for other positions
+       in the plan's bundles instead of ranking and pairing them itself.  A plan made for other positions
        gives wrong outputs and writes the new K/V rows at the plan's rows, never outside the
        arena.  One made for another batch gives NaN rows masked and is not used unmasked (the
        launch ranks by itself); one for another ctx or head shape gives NaN rows masked.
@@ -249,9 +249,11 @@ int q3t_decode_attention_static(const q3t_decode_args *args, void *stream);
    header of 32 ints (batch, M, segments per share, ctx, bit mask of requests with L_b = 0,
    zeros) follows the M shares.  A share holds at most min(8, 16 / (q_heads / kv_heads))
    segments and a request spans at most three shares; positions that need more get whole
-   requests paired longest with shortest instead.  The ranking section follows the header:
-   (batch, 0), then the pairs (b, L_b) of ranks 0 .. 127, longest first with ties by ascending
-   b ((-1, 0) past the batch); unmasked launches read it, masked ones the shares.
+   requests paired longest with shortest instead.  The bundle section follows the header:
+   (batch, 0), then for each of the M bundles (workgroups of a KV head) four (b, L_b) pairs
+   ((-1, 0): none), every request of the batch listed once: bundle m holds the requests of
+   length ranks m, 2M-1-m, 2M+m and 4M-1-m (longest first, ties by ascending b).  Unmasked
+   launches read the bundle section, masked ones the shares.
    batch <= 128, ctx <= 2^20, q_heads / kv_heads in {1, 2, 4};
    `plan` holds q3t_decode_plan_bytes bytes (16-byte aligned).  One small kernel on `stream`;
    it may be captured.  No counterpart in the reference (its attention operator takes no

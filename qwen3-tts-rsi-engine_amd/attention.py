@@ -140,7 +140,7 @@ PLAN_MAX_BATCH = 128  # requests a decode plan covers (the bundled grid's limit)
 def plan_shape(batch, q_heads, kv_heads):
     """Shape of the int32 plan ``decode_plan`` writes for a launch of these sizes: one
     dimension holding (shares, 8, 4) segment entries of every KV head's shares, a header of 32
-    ints and a ranking section of 258 ints (q3t_decode_plan); None when no plan covers the
+    ints and a bundle section of 2 + 8 * shares ints (q3t_decode_plan); None when no plan covers the
     shape."""
     nbytes = _lib.library().q3t_decode_plan_bytes(int(batch), int(q_heads), int(kv_heads))
     if nbytes <= 0:
@@ -157,8 +157,8 @@ def decode_plan(positions, capacity, q_heads, kv_heads, *, out=None):
     {1, 2, 4}).  The plan holds two cuts of the step's keys.  A masked launch reads the first:
     the keys of all requests, end to end in request order, cut into equal shares of whole
     64-key stages, one per workgroup of each KV head, a request cut between shares merged
-    through the launch's workspace.  An unmasked launch reads the second: the requests ranked
-    by length, whole requests per workgroup paired longest with shortest.  Returns an int32
+    through the launch's workspace.  An unmasked launch reads the second: whole requests per
+    workgroup, ranked by length and paired longest with shortest.  Returns an int32
     ``plan_shape`` tensor.
     One small kernel on the current stream (it can be captured); the plan stays valid while
     ``positions`` are unchanged: a plan of other positions gives wrong outputs."""

@@ -860,8 +860,8 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(const int32_t 
     const int h = blockIdx.x % hkv, m = blockIdx.x / hkv, M = bundles;
     // The plan entries of this bundle, the plan's batch and every line of the argument block in
     // one scalar round trip: the plan pointer and the sizes its addresses need are the leading
-    // kernel arguments, which the hardware preloads into scalar registers.  The plan's ranking
-    // section is (B, 0) and then the (b, L) pair of each rank.
+    // kernel arguments, which the hardware preloads into scalar registers.  The plan's bundle
+    // section is (B, 0) and then four (b, L) pairs per bundle.
     auto bundle_rank = [&](int i) { return (i >> 1) * 2 * M + ((i & 1) ? 2 * M - 1 - m : m); };
     uint64_t e[kBundleMaxSeg] = {0, 0, 0, 0};
     uint32_t plan_batch = 0;
@@ -870,7 +870,7 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(const int32_t 
         uint64_t a[kBundleMaxSeg];
 #pragma unroll
         for (int i = 0; i < kBundleMaxSeg; ++i)
-            a[i] = base + 8 + 8 * (uint64_t)(bundle_rank(i) < nb ? bundle_rank(i) : 0);
+            a[i] = base + 8 + 8 * (uint64_t)(m * kBundleMaxSeg + i);
         constexpr int BYTES = 32 + (int)sizeof(DecodeParams);
         static_assert(BYTES <= 8 * 64, "eight 64-byte lines at most");
         const uint64_t ka = reinterpret_cast<uint64_t>(__builtin_amdgcn_kernarg_segment_ptr());
@@ -917,13 +917,11 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(const int32_t 
         nseg = i + 1;
     };
     if (plan && (int)plan_batch == nb) {
-        // a ranking made once for the step's positions (q3t_decode_plan): (b, L) pairs, longest
-        // first, loaded above; no ranking here.  Entries that do not name a request of this
-        // batch attend nothing and write nothing (ranks past the batch read entry 0 and are
-        // ignored).  A plan made for another batch is not used: the launch ranks by itself.
+        // the bundle's requests as the step's plan lists them (q3t_decode_plan), loaded above;
+        // no ranking here.  Entries that do not name a request of this batch attend nothing and
+        // write nothing.  A plan made for another batch is not used: the launch ranks by itself.
 #pragma unroll
         for (int i = 0; i < kBundleMaxSeg; ++i) {
-            if (bundle_rank(i) >= p.B) continue;
             const int b = (int)(uint32_t)e[i], L = (int)(uint32_t)(e[i] >> 32);
             const bool ok = b >= 0 && b < p.B;
             set_slot(i, ok ? b : -1, ok ? min(max(L, 0), p.ctx) : 0);

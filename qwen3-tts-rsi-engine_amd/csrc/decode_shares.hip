@@ -785,9 +785,9 @@ decode_shares_kernel(const int32_t *plan, int nb, int hkv, int M, DecodeParams p
 // ---- the plan: one launch per step, read by every layer ---------------------------------
 // plan[(m * 8 + k) * 4 ...] = (b, j0, j1, info) for segment k of share m (b = -1: none), and
 // after the M shares a header of 32 ints (batch, M, segment cap, ctx, four words of the bit
-// mask of requests without a valid position, zeros), then the ranking section that the
-// whole-request kernel of an unmasked launch reads: (batch, 0) and 128 pairs (b, L_b) in rank
-// order, longest first, ties by ascending b ((-1, 0) for ranks past the batch).  L_b = pos[b] + 1 for a position
+// mask of requests without a valid position, zeros), then the bundle section that the
+// whole-request kernel of an unmasked launch reads: (batch, 0) and, for each of the M bundles,
+// four (b, L_b) pairs ((-1, 0): none), every request of the batch in one of them.  L_b = pos[b] + 1 for a position
 // in [0, ctx), else 0.
 constexpr int kPlanThreads = kMaxBatch;
 
@@ -811,6 +811,7 @@ decode_shares_plan_kernel(const int64_t *pos, int B, int ctx, int M, int cap, in
     __shared__ int sL[kMaxBatch], pre[kMaxBatch + 1], ne[kMaxBatch + 1];
     __shared__ int first[kMaxBundles], count[kMaxBundles], cut[kMaxBundles];
     __shared__ __attribute__((aligned(16))) int keys[kMaxBatch];
+    __shared__ int sorted_b[kMaxBatch], sorted_l[kMaxBatch];
     __shared__ int part[2][2];
     __shared__ int fallback;
     __shared__ uint32_t zmask[4];
@@ -915,7 +916,8 @@ decode_shares_plan_kernel(const int64_t *pos, int B, int ctx, int M, int cap, in
             const int4 k4 = *reinterpret_cast<const int4 *>(&keys[j]);  // keys past B are -1
             rank += (k4.x > key) + (k4.y > key) + (k4.z > key) + (k4.w > key);
         }
-        reinterpret_cast<int2 *>(plan + (M + 1) * kSlots * 4)[1 + rank] = int2{t, L};
+        sorted_b[rank] = t;
+        sorted_l[rank] = L;
         if (fallback && L > 0) {
             const int round = rank / M, within = rank % M;
             const int mm = (round & 1) ? M - 1 - within : within;
@@ -925,10 +927,15 @@ decode_shares_plan_kernel(const int64_t *pos, int B, int ctx, int M, int cap, in
     __syncthreads();
     int4 *entries = reinterpret_cast<int4 *>(plan);
     for (int i = t; i < M * kSlots; i += kPlanThreads) entries[i] = ent[i];
-    int2 *ranking = reinterpret_cast<int2 *>(plan + (M + 1) * kSlots * 4);
-    if (t >= B) ranking[1 + t] = int2{-1, 0};
+    // whole requests: bundle m takes ranks m, 2M-1-m, 2M+m, 4M-1-m (longest with shortest)
+    int2 *bundles = reinterpret_cast<int2 *>(plan + (M + 1) * kSlots * 4);
+    for (int i = t; i < M * 4; i += kPlanThreads) {
+        const int mm = i / 4, k = i % 4;
+        const int r = (k >> 1) * 2 * M + ((k & 1) ? 2 * M - 1 - mm : mm);
+        bundles[1 + i] = r < B ? int2{sorted_b[r], sorted_l[r]} : int2{-1, 0};
+    }
     if (t == 0) {
-        ranking[0] = int2{B, 0};
+        bundles[0] = int2{B, 0};
         int32_t *hd = plan + M * kSlots * 4;
         hd[0] = B;
         hd[1] = M;
@@ -975,7 +982,7 @@ int64_t shares_rank_offset(int64_t batch, int64_t kv_heads) {
     return (shares::bundle_count(batch, kv_heads) + 1) * shares::kSlots * 4;
 }
 int64_t shares_plan_ints(int64_t batch, int64_t kv_heads) {
-    return shares_rank_offset(batch, kv_heads) + 2 + 2 * shares::kMaxBatch;
+    return shares_rank_offset(batch, kv_heads) + 2 + 8 * shares::bundle_count(batch, kv_heads);
 }
 int64_t shares_partial_floats(int64_t batch, int64_t kv_heads, int64_t group) {
     return kv_heads * shares::bundle_count(batch, kv_heads) * shares::kWaves * (group * 128 + 8);

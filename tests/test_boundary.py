@@ -88,14 +88,16 @@ def test_rejected_calls_return_negative_status_without_a_gpu(pkg):
     assert lib.q3t_decode_plan(16, 4, 1024, 24, 8, 16, None) == -1        # 3 query heads per KV head
     assert lib.q3t_decode_plan(16, 4, 1024, 16, 8, 8, None) == -1         # plan not 16-byte aligned
     assert lib.q3t_decode_plan(None, 0, 1024, 16, 8, None, None) == 0     # an empty batch launches nothing
-    # the plan's size: 32 shares per KV head of 8 (one workgroup per CU) and a header row,
+    # the plan's size: M = 32 shares per KV head of 8 (one workgroup per CU) and a header row,
     # 8 entries of 16 bytes each (more shares when a batch needs more than 4 requests per
-    # share), then the ranking section: (batch, 0) and 128 (b, L) pairs of 4-byte ints
-    ranking = (2 + 2 * 128) * 4
-    assert lib.q3t_decode_plan_bytes(64, 16, 8) == 33 * 8 * 16 + ranking
-    assert lib.q3t_decode_plan_bytes(128, 16, 16) == 33 * 8 * 16 + ranking
-    assert lib.q3t_decode_plan_bytes(128, 64, 64) == 33 * 8 * 16 + ranking
-    assert lib.q3t_decode_plan_bytes(128, 4, 4) == 65 * 8 * 16 + ranking
+    # share), then the bundle section: (batch, 0) and four (b, L) pairs of 4-byte ints for
+    # each of the M bundles
+    def size(shares):
+        return (shares + 1) * 8 * 16 + 8 + shares * 4 * 8
+    assert lib.q3t_decode_plan_bytes(64, 16, 8) == size(32)
+    assert lib.q3t_decode_plan_bytes(128, 16, 16) == size(32)
+    assert lib.q3t_decode_plan_bytes(128, 64, 64) == size(32)
+    assert lib.q3t_decode_plan_bytes(128, 4, 4) == size(64)
     assert lib.q3t_decode_plan_bytes(64, 24, 8) == -1
     # the allocation-free entry point refuses, before touching any device, a call whose split
     # states would not fit its fixed 8 MiB array (1024 requests x 8 heads x 16 chunks)

@@ -144,8 +144,8 @@ def test_bundled_grid_edges(pkg, device, group, batch, capacity, fused):
     idx = np.flatnonzero(valid.numpy())
     expected = oatt.decode_attention(query[idx], keys[idx], values[idx], contexts.numpy()[idx], D ** -0.5)
     assert_attention_close(got[idx], expected)
-    # the same launch from the step's plan: its ranking is the one the launch makes itself,
-    # so the outputs are bit-identical; and masked by SlotGraph.compute's mask (0 up to each
+    # the same launch from the step's plan: each request is still scored whole by one
+    # workgroup in the same order, so the outputs are bit-identical; and masked by SlotGraph.compute's mask (0 up to each
     # position, the most negative bf16 after), the plan's equal shares of each head's keys
     # (requests cut between shares merged through the workspace): the same arena rows,
     # outputs in the bar
@@ -169,17 +169,17 @@ def test_bundled_grid_edges(pkg, device, group, batch, capacity, fused):
 
 
 SLOTS, LAST, MERGE, PUBLISH = 8, 1, 2, 4
-RANKS = 128
+PER_BUNDLE = 4
 
 
 def plan_parts(plan):
-    """Views of a plan tensor: the shares' segment entries (shares, 8, 4), the 32-int header
-    and the ranking section (129, 2): (batch, 0), then (b, L) of each rank."""
-    shares = (plan.numel() - 2 - 2 * RANKS) // (SLOTS * 4) - 1
+    """Views of a plan tensor: the shares' segment entries (M, 8, 4), the 32-int header and
+    the bundle section (1 + 4 M, 2): (batch, 0), then four (b, L) pairs per bundle."""
+    shares = (plan.numel() - 2 - SLOTS * 4) // (SLOTS * 4 + 2 * PER_BUNDLE)
     entries = plan[:shares * SLOTS * 4].view(shares, SLOTS, 4)
     header = plan[shares * SLOTS * 4:(shares + 1) * SLOTS * 4]
-    ranking = plan[(shares + 1) * SLOTS * 4:].view(RANKS + 1, 2)
-    return entries, header, ranking
+    bundles = plan[(shares + 1) * SLOTS * 4:].view(1 + PER_BUNDLE * shares, 2)
+    return entries, header, bundles
 
 
 def check_plan(plan, contexts, capacity, q_heads, kv_heads):
@@ -188,10 +188,11 @@ def check_plan(plan, contexts, capacity, q_heads, kv_heads):
     slots, at most 16 / group of them; a request cut between shares has its earlier parts in
     the first slot of the shares before (published) and its last part in the last slot of its
     final share (merging them); and, unless it fell back to whole requests, shares of whole
-    64-key stages within one stage of each other, the last one excepted.  The ranking section
-    lists every request once, by length descending with ties by index, (-1, 0) past the batch.
-    Returns (fell back, stages per share)."""
-    entries, header, ranking = (t.cpu().numpy() for t in plan_parts(plan))
+    64-key stages within one stage of each other, the last one excepted.  The bundle section
+    lists every request of the batch once, with its length, in at most four slots per bundle
+    ((-1, 0) elsewhere), and no bundle holds more keys than pairing the i-th longest request
+    with the i-th shortest gives.  Returns (fell back, stages per share)."""
+    entries, header, bundles = (t.cpu().numpy() for t in plan_parts(plan))
     e = entries
     shares = e.shape[0]
     batch = len(contexts)
@@ -200,10 +201,17 @@ def check_plan(plan, contexts, capacity, q_heads, kv_heads):
     assert list(header[:4]) == [batch, shares, cap, capacity] and not header[8:].any()
     zero = sum(1 << b for b in range(batch) if lengths[b] == 0)
     assert sum(int(np.uint32(header[4 + w])) << (32 * w) for w in range(4)) == zero
+    assert list(bundles[0]) == [batch, 0]
+    table = bundles[1:].reshape(-1, PER_BUNDLE, 2)
+    listed = sorted(int(b) for b in table[:, :, 0].reshape(-1) if b >= 0)
+    assert listed == list(range(batch))
+    assert all(table[m, k, 1] == lengths[table[m, k, 0]] for m, k in zip(*np.nonzero(table[:, :, 0] >= 0)))
+    assert ((table[:, :, 0] >= 0) | (table[:, :, 1] == 0)).all()
     order = sorted(range(batch), key=lambda b: (-lengths[b], b))
-    assert list(ranking[0]) == [batch, 0]
-    assert [tuple(r) for r in ranking[1:batch + 1]] == [(b, lengths[b]) for b in order]
-    assert (ranking[batch + 1:] == [-1, 0]).all()
+    bundles_m = table.shape[0]
+    paired = [sum(lengths[order[r]] for r in (m, 2 * bundles_m - 1 - m, 2 * bundles_m + m, 4 * bundles_m - 1 - m)
+                  if r < batch) for m in range(bundles_m)]
+    assert table[:, :, 1].sum(1).max() <= max(paired)
     covered = [np.zeros(n, int) for n in lengths]
     keys, whole = [], True
     for m in range(shares):
@@ -289,15 +297,15 @@ def test_decode_plan_of_other_positions_stays_in_bounds(pkg, device, masked):
     allowed = {(b, h, int(stale_ctx[b])) for b in range(64) for h in range(HKV)}
     assert changed.shape[0] > 0 and {tuple(int(x) for x in r) for r in changed} <= allowed
     bad = stale.clone()
-    entries, _, ranking = plan_parts(bad)
+    entries, _, bundles = plan_parts(bad)
     if masked:
         entries[::3, 0, 0] = 1000     # no such request: the share lists nothing
         entries[1::3, 0, 2] = 5000    # more keys than the arena has: clamped
         named = set(int(b) for b in entries[:, :, 0].reshape(-1).cpu().tolist() if 0 <= b < 64)
     else:
-        ranking[1::3, 0] = 1000       # no such request: the rank attends nothing
-        ranking[2::3, 1] = 5000       # more keys than the arena has: clamped
-        named = set(int(b) for b in ranking[1:65, 0].cpu().tolist() if 0 <= b < 64)
+        bundles[1::3, 0] = 1000       # no such request: the slot attends nothing
+        bundles[2::3, 1] = 5000       # more keys than the arena has: clamped
+        named = set(int(b) for b in bundles[1:, 0].cpu().tolist() if 0 <= b < 64)
     out = torch.full((64, 1, HQ, D), 7.0, device=device, dtype=torch.bfloat16)
     pkg.decode_attention(q, k, v, positions, grid="bundled", plan=bad, out=out, mask=mask)
     torch.cuda.synchronize()

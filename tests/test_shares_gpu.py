@@ -1,7 +1,6 @@
 """The bundled grid's masked launches, which run on the step's plan (equal shares of each KV
 head's keys, every request of a share scored as its own MFMA columns, requests cut between
-shares merged through the workspace), against the float64 oracle; and the plan's ranking,
-which the unmasked launches of a step read.
+shares merged through the workspace), against the float64 oracle.
 
 The reference's masked talker flow is covered at full size: SlotGraph.compute builds the
 (B, 1, 1, ctx) mask 0 / finfo.min for keys j <= pos[b] every step and hands it to every layer

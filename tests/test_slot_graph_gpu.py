@@ -198,9 +198,9 @@ def test_mask_is_built_only_for_unwrapped_layers(pkg, device):
 def test_talker_step_on_the_bundled_grid_reads_the_step_plan(pkg, device):
     """At the talker's shape (64 slots of a 1024-row arena, 8 KV heads of 128: the bundled
     grid) SlotCache.prepare plans the step once (decode_plan) and every layer's launch reads
-    the plan's ranking: replays equal an eager twin whose cache holds no plan (each launch
-    ranks the requests itself), output and arena bit-identical, and the ranking equals a
-    stable sort by length."""
+    the plan's bundles of whole requests: replays equal an eager twin whose cache holds no
+    plan (each launch ranks and pairs the requests itself), output and arena bit-identical,
+    and the bundles list every request once with its length."""
     slots, capacity, batch = 64, 1024, 64
     model = _model(pkg, device, layers=2)
     arena = _arena(pkg, model, slots, capacity, 24)
@@ -226,9 +226,10 @@ def test_talker_step_on_the_bundled_grid_reads_the_step_plan(pkg, device):
         torch.cuda.synchronize()
         assert twin.cache.plan is None and graph.cache.plan is not None
         lengths = positions.numpy() + 1
-        order = np.lexsort((np.arange(batch), -lengths))
-        ranking = plan_parts(graph.cache.plan)[2].cpu().numpy()
-        np.testing.assert_array_equal(ranking[1:batch + 1], np.stack([order, lengths[order]], 1))
+        table = plan_parts(graph.cache.plan)[2].cpu().numpy()[1:]
+        listed = table[table[:, 0] >= 0]
+        np.testing.assert_array_equal(np.sort(listed[:, 0]), np.arange(batch))
+        np.testing.assert_array_equal(listed[:, 1], lengths[listed[:, 0]])
         assert np.array_equal(bits(out), bits(expected)), f"step {step}"
         assert np.array_equal(bits(arena.packed), bits(twin_arena.packed)), f"step {step}"
     graph.close()
