@@ -542,7 +542,7 @@ def main():
     attn_us = start.elapsed_time(stop) * 1e3 / (reps * LAYERS)
 
     # the reference's own flow: SlotGraph.compute hands every layer the (B, 1, 1, ctx) additive
-    # mask j <= pos[b] (continuous.py:188-197), a masked launch (the shares kernel)
+    # mask j <= pos[b] (continuous.py:188-197): a masked launch of the bundled grid
     allowed = torch.arange(CAPACITY, device=device)[None, :] <= positions[:, None]
     ref_mask = torch.where(allowed, 0.0, torch.finfo(torch.bfloat16).min).to(torch.bfloat16)[:, None, None, :]
     masked_graph = torch.cuda.CUDAGraph()

@@ -121,12 +121,10 @@ int q3t_rope_tables(const int64_t *positions, int64_t n, const float *inv_freq, 
  *
  * Three grids compute the same result (to rounding; `grid` picks one, Q3T_GRID_*):
  *   - bundled: one workgroup per CU, streaming keys through LDS and scoring them on bf16
- *     MFMA tiles.  Unmasked, each workgroup takes whole requests, longest paired with
- *     shortest, ranked by the step's `plan` (q3t_decode_plan) or, without one, by the
- *     workgroup itself.  Masked (unit key stride, 4-byte aligned; the call must bring the
- *     plan), each workgroup streams an equal share of one KV head's concatenated keys, every
- *     request of the share scored at once as its own MFMA columns, and the requests cut
- *     between shares merge through `workspace`.  bf16, head_dim 128, query_len 1,
+ *     MFMA tiles.  Each workgroup takes whole requests of one KV head, longest paired with
+ *     shortest, as the step's `plan` (q3t_decode_plan) bundles them or, without one, as the
+ *     workgroup ranks them itself.  A mask needs unit key stride and 4-byte alignment (bf16
+ *     masks take a branch-free path).  bf16, head_dim 128, query_len 1,
  *     q_heads / kv_heads <= 4, batch <= 128.  The
  *     default for 64..128 requests (times kv_heads >= 512) over 1024 <= ctx < 2048 (the
  *     talker's 1024-row arena).
@@ -201,14 +199,12 @@ typedef struct q3t_decode_args {
     /* Q3T_GRID_AUTO (0), Q3T_GRID_CHUNKED, Q3T_GRID_BALANCED or Q3T_GRID_BUNDLED; a grid the
        call does not qualify for returns Q3T_EUNSUPPORTED */
     int64_t grid;
-    /* bundled grid, optional (required with a mask): the plan q3t_decode_plan wrote for these
-       `positions`, `batch`, `ctx`, `q_heads` and `kv_heads` (device, q3t_decode_plan_bytes).
-       A masked launch streams the plan's equal shares of each KV head's keys (requests cut
-       between shares are merged through the workspace); an unmasked one takes whole requests
-       in the plan's bundles instead of ranking and pairing them itself.  A plan made for other positions
-       gives wrong outputs and writes the new K/V rows at the plan's rows, never outside the
-       arena.  One made for another batch gives NaN rows masked and is not used unmasked (the
-       launch ranks by itself); one for another ctx or head shape gives NaN rows masked.
+    /* bundled grid, optional: the plan q3t_decode_plan wrote for these `positions`, `batch`,
+       `ctx` and `kv_heads` (device, q3t_decode_plan_bytes): the launch takes whole requests
+       as the plan bundles them instead of ranking and pairing them itself.  A plan made for
+       other positions gives wrong outputs, and a fused launch then writes the new K/V rows
+       at the rows the plan names (the last key of each request it lists), never outside the
+       arena.  One made for another batch is not used (the launch ranks by itself).
        Ignored by the other grids. */
     const int32_t *plan;
 } q3t_decode_args;
@@ -242,23 +238,16 @@ int q3t_decode_attention_static(const q3t_decode_args *args, void *stream);
 
 /* The bundled grid's plan of a step, written once per step and passed as `plan` to every
    layer's launch of that step (the talker's layers all attend the same lengths).  With
-   L_b = positions[b] + 1 for a position in [0, ctx) and 0 otherwise, the keys of all requests
-   laid end to end in request order are cut into M shares of whole 64-key stages (M =
-   max(ceil(256 / kv_heads), ceil(batch / 4)) per KV head, one workgroup per CU); share m's
-   entries are up to 8 segments (request b, keys [j0, j1), flags) at int32 offset 32 m, and a
-   header of 32 ints (batch, M, segments per share, ctx, bit mask of requests with L_b = 0,
-   zeros) follows the M shares.  A share holds at most min(8, 16 / (q_heads / kv_heads))
-   segments and a request spans at most three shares; positions that need more get whole
-   requests paired longest with shortest instead.  The bundle section follows the header:
-   (batch, 0), then for each of the M bundles (workgroups of a KV head) four (b, L_b) pairs
-   ((-1, 0): none), every request of the batch listed once: bundle m holds the requests of
-   length ranks m, 2M-1-m, 2M+m and 4M-1-m (longest first, ties by ascending b).  Unmasked
-   launches read the bundle section, masked ones the shares.
-   batch <= 128, ctx <= 2^20, q_heads / kv_heads in {1, 2, 4};
-   `plan` holds q3t_decode_plan_bytes bytes (16-byte aligned).  One small kernel on `stream`;
-   it may be captured.  No counterpart in the reference (its attention operator takes no
-   per-step state; positions are fixed for a step's layers in SlotGraph.compute,
-   continuous.py:188-198). */
+   L_b = positions[b] + 1 for a position in [0, ctx) and 0 otherwise, and M =
+   max(ceil(256 / kv_heads), ceil(batch / 4)) workgroups (bundles) per KV head, one per CU:
+   plan[0] = batch, plan[1] = M, then for each bundle m four (b, L_b) int32 pairs ((-1, 0):
+   none), every request of the batch listed once: bundle m holds the requests of length ranks
+   m, 2M-1-m, 2M+m and 4M-1-m (longest first, ties by ascending b), so the i-th longest
+   request shares a workgroup with the i-th shortest.  batch <= 128, ctx <= 2^20,
+   q_heads / kv_heads <= 4; `plan` holds q3t_decode_plan_bytes bytes (16-byte aligned).
+   One small kernel on `stream`; it may be captured.  No counterpart in the reference (its
+   attention operator takes no per-step state; positions are fixed for a step's layers in
+   SlotGraph.compute, continuous.py:188-198). */
 int q3t_decode_plan(const int64_t *positions, int64_t batch, int64_t ctx, int64_t q_heads, int64_t kv_heads,
                     int32_t *plan, void *stream);
 

@@ -111,12 +111,11 @@ def _grid_code(grid):
 
 
 def decode_grid_for(batch, query_len, q_heads, kv_heads, head_dim, ctx, dtype=torch.bfloat16, *,
-                    masked=False, splits=0, grid=None, planned=True):
+                    masked=False, splits=0, grid=None):
     """Name of the grid a decode call of these sizes runs on ('bundled', 'balanced' or
     'chunked'), as the library chooses it (q3t_decode_grid); ValueError when a named grid does
     not take such a call.  ``masked``: a contiguous (batch, 1, ctx) bf16 mask, as
-    SlotGraph.compute builds it; ``planned``: the call brings the step's ``decode_plan`` (the
-    slot cache's talker step does)."""
+    SlotGraph.compute builds it."""
     a = _lib.DecodeArgs()
     a.batch, a.query_len, a.q_heads, a.kv_heads, a.head_dim, a.ctx = batch, query_len, q_heads, kv_heads, head_dim, ctx
     a.dtype = _lib.DTYPE_CODES[dtype]
@@ -126,7 +125,6 @@ def decode_grid_for(batch, query_len, q_heads, kv_heads, head_dim, ctx, dtype=to
     if masked:
         a.mask, a.mask_dtype = 16, _lib.Q3T_BF16
         a.mask_stride_b, a.mask_stride_s, a.mask_stride_t = ctx, ctx, 1
-    a.plan = 16 if planned else None
     a.splits, a.grid = int(splits), _grid_code(grid)
     code = _lib.library().q3t_decode_grid(a)
     if code < 0:
@@ -139,9 +137,8 @@ PLAN_MAX_BATCH = 128  # requests a decode plan covers (the bundled grid's limit)
 
 def plan_shape(batch, q_heads, kv_heads):
     """Shape of the int32 plan ``decode_plan`` writes for a launch of these sizes: one
-    dimension holding (shares, 8, 4) segment entries of every KV head's shares, a header of 32
-    ints and a bundle section of 2 + 8 * shares ints (q3t_decode_plan); None when no plan covers the
-    shape."""
+    dimension holding (batch, M) and four (request, length) pairs for each of the M bundles
+    (workgroups) of a KV head (q3t_decode_plan); None when no plan covers the shape."""
     nbytes = _lib.library().q3t_decode_plan_bytes(int(batch), int(q_heads), int(kv_heads))
     if nbytes <= 0:
         return None
@@ -153,13 +150,9 @@ def decode_plan(positions, capacity, q_heads, kv_heads, *, out=None):
     ``plan=`` to every layer's ``decode_step`` / ``decode_attention`` of that step (the layers
     of a talker step all attend the same lengths, SlotGraph.compute, continuous.py:188-198).
     positions (B,) int64 with B <= 128, capacity: the arena's rows (a position at or past it
-    attends nothing), q_heads / kv_heads: the attention's heads (q_heads / kv_heads in
-    {1, 2, 4}).  The plan holds two cuts of the step's keys.  A masked launch reads the first:
-    the keys of all requests, end to end in request order, cut into equal shares of whole
-    64-key stages, one per workgroup of each KV head, a request cut between shares merged
-    through the launch's workspace.  An unmasked launch reads the second: whole requests per
-    workgroup, ranked by length and paired longest with shortest.  Returns an int32
-    ``plan_shape`` tensor.
+    attends nothing), q_heads / kv_heads: the attention's heads (q_heads / kv_heads <= 4).
+    The requests are ranked by length and bundled, whole, one bundle per workgroup of each KV
+    head, the i-th longest with the i-th shortest.  Returns an int32 ``plan_shape`` tensor.
     One small kernel on the current stream (it can be captured); the plan stays valid while
     ``positions`` are unchanged: a plan of other positions gives wrong outputs."""
     if positions.ndim != 1 or positions.dtype != torch.int64:
@@ -171,7 +164,7 @@ def decode_plan(positions, capacity, q_heads, kv_heads, *, out=None):
         raise ValueError('capacity must be in [1, 2^20]')
     shape = plan_shape(batch, q_heads, kv_heads)
     if shape is None:
-        raise ValueError('a decode plan needs q_heads / kv_heads in {1, 2, 4}')
+        raise ValueError('a decode plan needs q_heads a multiple of kv_heads, at most 4 per KV head')
     device = _lib.require_gpu(positions)
     if not positions.is_contiguous():
         positions = positions.contiguous()
@@ -203,10 +196,9 @@ def decode_attention(query, keys, values, positions, *, scale=None, mask=None, k
     """query (B, S, Hq, D) BSND; keys/values (B, Hkv, ctx, D) views of the arena (or, with
     ``kv_offsets``, any base tensor whose request rows start at those element offsets);
     positions (B,) int64: the last query position of each request.  ``grid`` picks the
-    kernel grid: 'bundled' (one workgroup per CU streaming through LDS onto bf16 MFMA tiles: with
-    a mask and ``plan``, equal shares of each head's keys; without a mask, whole requests in
-    length-balanced bundles, ranked by ``plan`` when given; one query token, head_dim 128, up to
-    128 requests), 'balanced'
+    kernel grid: 'bundled' (one workgroup per CU streaming through LDS onto bf16 MFMA tiles: whole
+    requests in length-balanced bundles, bundled by ``plan`` when given; a mask with unit key
+    stride; one query token, head_dim 128, up to 128 requests), 'balanced'
     (equal shares of each head's keys over ``splits`` workgroups per head, 0: 256 in all),
     'chunked' (chunks of 64-key blocks per request, at most ``max_chunks``, 0: enough for
     ~512 workgroups) or None for the library's choice, in which ``splits`` > 0 / < 0 still

@@ -831,6 +831,7 @@ struct BundleLds {
     float ml[2][kWaves][G][2];
     alignas(16) uint16_t outq[kBundleMaxSeg][G][128];  // bf16 outputs, stored after the stream
     alignas(16) int keys[kWaves][kBundleMaxBatch];  // each wave's copy of the ranking keys
+    uint32_t maskw[kRingStages][kWaves][64];        // masked: the mask words of a stage's rows
 };
 
 // The bundle's requests as wave-uniform values (scalar registers): request index, length and
@@ -850,9 +851,17 @@ struct Slots4 {
 };
 
 // NORM: the fused q/k RMSNorm is compiled in (a separate instance: its code, even unexecuted,
-// cost the talker step 1.8 us per launch in the instance without norms).
-template <int G, bool FUSED, bool STREAM, bool NORM>
+// cost the talker step 1.8 us per launch in the instance without norms).  MASK: an additive or
+// bool (batch, 1, ctx) mask with unit key stride is added to the scores of keys 0 ... pos[b]
+// (SlotGraph.compute hands every layer one, continuous.py:188-197): each wave loads the mask
+// words of its 16 rows of a stage with the stage, one 4-byte load per row into LDS.  MK: 0 no
+// mask, 1 a bf16 mask (SlotGraph.compute's, in the model's dtype: a branch-free term), 2 any
+// other dtype.  With one wave per SIMD the scoring instructions sit on each stage's critical
+// path, so the terms' byte offsets are fixed once per request (keys 4g ... 4g+3 of a lane start
+// at a multiple of 4): a per-element 64-bit index and dtype switch cost the talker step 3.9 us.
+template <int G, bool FUSED, bool STREAM, bool NORM, int MK>
 __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(const int32_t *plan, int nb, int hkv, int bundles, DecodeParams p) {
+    constexpr bool MASK = MK != 0;
     static_assert(G >= 1 && G <= 4, "query rows are the first G of 16 MFMA columns, four LDS rows");
     __shared__ __attribute__((aligned(16))) BundleLds<G> s;
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
@@ -998,10 +1007,19 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(const int32_t 
     // producer: the next stage to load (request slot ps, first key pj); rows at or past the
     // request's keys get offsets outside the resource (zeros, no memory access).  The request's
     // resources and key counts stay in scalar registers from one stage to the next.
-    int ps = first_live, pj = 0, pL = 0, pjend = 0;
+    int ps = first_live, pj = 0, pL = 0, pjend = 0, pb = 0;
     i32x4_t krs, vrs;
+    constexpr int KL = kStageLoads + (MASK ? 1 : 0);  // loads per wave and stage
+    const int mes = MASK ? mask_elem_size(p.mask_dtype) : 0;
+    i32x4_t mrs = {0, 0, 0, 0};
+    if constexpr (MASK) {
+        const uint32_t mbytes = (uint32_t)((((int64_t)(nb - 1) * p.m_sb + p.ctx) * mes + 3) & ~(int64_t)3);
+        mrs = scalar_rsrc(p.mask, mbytes);
+    }
+    const uint32_t lds_mask = (uint32_t)(uintptr_t)&s.maskw[0][0][0];
     auto producer_request = [&]() {
         pL = seg_l(ps);
+        pb = seg_b(ps);
         pjend = FUSED ? pL - 1 : pL;  // fused: row L-1 is the step's own key
         krs = scalar_rsrc(seg_row0(p.k, tb_k, ps), kbytes);
         vrs = scalar_rsrc(seg_row0(p.v, tb_v, ps), vbytes);
@@ -1026,6 +1044,14 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(const int32_t 
                 load_to_lds16(krs, ko, kl);
                 load_to_lds16(vrs, vo, vl);
             }
+        }
+        if constexpr (MASK) {
+            // the mask word of each of the wave's 16 rows (lane r: row r); rows past the
+            // request's keys read zeros
+            const int q = pj + wave * kWaveKeys + (lane & 15);
+            const int64_t elem = (int64_t)pb * p.m_sb + q;
+            const uint32_t off = (lane < 16 && q < pL) ? (uint32_t)((elem * mes) & ~(int64_t)3) : 0xfffffff0u;
+            load_to_lds4(mrs, off, (uint32_t)__builtin_amdgcn_readfirstlane((int)(lds_mask + (slot * kWaves + wave) * 256)));
         }
         pj += kStageKeys;
         if (pj >= pL) {
@@ -1074,8 +1100,8 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(const int32_t 
 
     {
         // the rows landed before the stages (which stay in flight)
-        if (issued == 1) wait_loads<kStageLoads>();
-        else wait_loads<2 * kStageLoads>();
+        if (issued == 1) wait_loads<KL>();
+        else wait_loads<2 * KL>();
         if constexpr (FUSED) {
             // each request's rows in the wave that loaded them, while the first stages are in
             // flight: lane group r < G holds query row r and lane group G the step's key (a
@@ -1121,6 +1147,7 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(const int32_t 
     float mx = kEmpty, l = 0.f;
     f32x4_t acc[8];
     int cs = first_live, cj = 0, par = 0;
+    uint32_t msub = 0;  // masked: the byte offsets of the current request's mask terms
     int L = seg_l(cs);  // the consumer's request: its keys and rows, kept between stages
     uint32_t hd = head_of(cs);
     for (int t = 0; t < total; ++t) {
@@ -1128,6 +1155,13 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(const int32_t 
         if (issued < total && issued <= t + 1) issue_next();
         const int ahead = issued - 1 - t;  // stages issued after this one: 0 or 1
         if (cj == 0) {
+            if constexpr (MASK) {
+                // byte offsets within their words of the lane's keys 4g + i of any stage (one byte each)
+                const int64_t e0 = (int64_t)seg_b(cs) * p.m_sb;
+                msub = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) msub |= (uint32_t)(((e0 + i) * mes) & 3) << (8 * i);
+            }
             // a new request: its rows as B operands, columns c >= G zero
             const U4 zero = {0u, 0u, 0u, 0u};
             const int cq = c < G ? c : 0;
@@ -1143,7 +1177,7 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(const int32_t 
         }
         // this stage has landed (the next one stays in flight)
         if (ahead == 0) wait_loads<0>();
-        else wait_loads<kStageLoads>();
+        else wait_loads<KL>();
         if constexpr (FUSED) {
             if (t == 0) {
                 // the step's keys and values into the arena, by each request's wave, only now: a
@@ -1182,8 +1216,24 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(const int32_t 
             st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(lds_read16(sb + ka[kk])), qB[kk], st, 0, 0, 0);
         const int j0 = cj + wave * kWaveKeys + 4 * g;
         float x[4];
+        if constexpr (MASK) {
+            const U4 w4 = lds_read16(lds_mask + ((t % kRingStages) * kWaves + wave) * 256 + 16 * g);
+            const uint32_t wv[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) x[i] = j0 + i < L ? st[i] * scale : -INFINITY;
+            for (int i = 0; i < 4; ++i) {
+                float term;
+                if constexpr (MK == 1) {
+                    // bf16: the element is the word's high half at byte offset 2, else its low half
+                    term = __uint_as_float((msub >> (8 * i)) & 2u ? (wv[i] & 0xffff0000u) : (wv[i] << 16)) * kLog2e;
+                } else {
+                    term = mask_term(wv[i], (msub >> (8 * i)) & 3u, p.mask_dtype);
+                }
+                x[i] = j0 + i < L ? st[i] * scale + term : -INFINITY;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = j0 + i < L ? st[i] * scale : -INFINITY;
+        }
         float mb = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
         mb = fmaxf(mb, xor16(mb));
         mb = fmaxf(mb, xor32(mb));
@@ -1318,8 +1368,8 @@ static int64_t chunk_count(int64_t batch, int64_t kv_heads, int64_t ctx, int64_t
 
 // The grid a call runs on (Q3T_GRID_CHUNKED, _BALANCED or _BUNDLED; -1: a requested grid the
 // call does not qualify for).  The bundled grid needs bf16 rows of 128, one query token, at
-// most kBundleMaxBatch requests, q_heads / kv_heads <= 4, and a mask only where the shares
-// kernel takes the call.  Automatic choice,
+// most kBundleMaxBatch requests, q_heads / kv_heads <= 4, and a mask with unit key stride.
+// Automatic choice,
 // measured (bf16, 16/8 heads, fused and unfused): bundled for 64..128 requests over arenas of
 // 1024 to 2047 rows (64 requests over 1024 rows: 27.6 us against 30.0 chunked and 37.9
 // balanced; 128 requests: 50.4 against 52.1 and 54.8); balanced from 2048 rows (128 requests
@@ -1327,28 +1377,16 @@ static int64_t chunk_count(int64_t batch, int64_t kv_heads, int64_t ctx, int64_t
 // fewer requests (128 requests over 512 rows: 32.0 against 33.9 bundled; 32 over 1024: 21.6
 // against 21.8), where the bundled grid's ranking and start-up are not repaid.
 constexpr int64_t kBundleMinCtx = 1024;
-// A masked bundled launch runs the shares kernel (decode_shares.hip), an unmasked one the
-// whole-request kernel above.  The shares kernel takes a call that brings the step's plan
-// (q3t_decode_plan) and whose arena rows can be addressed from one base per KV head: no
-// per-request offsets, identical key and value layouts, and every request's rows of a head
-// within 4 GiB of request 0's; a mask needs unit key stride and 4-byte alignment.
-static bool shares_ok(const q3t_decode_args *a) {
-    if (!a->plan || a->kv_offsets || a->k_stride_b != a->v_stride_b || a->k_stride_h != a->v_stride_h ||
-        a->k_stride_t != a->v_stride_t || a->k_stride_b < 0 || a->k_stride_t < 0)
-        return false;
-    const int64_t g = a->q_heads / a->kv_heads;
-    if (g != 1 && g != 2 && g != 4) return false;
-    if ((a->batch - 1) * a->k_stride_b * 2 + (a->ctx - 1) * a->k_stride_t * 2 + 256 > (int64_t)UINT32_MAX) return false;
-    if (shares_flag_count(a->batch, a->kv_heads) > kMaxCounters) return false;
-    if (a->mask) {
-        const int64_t es = a->mask_dtype == Q3T_F32 ? 4 : a->mask_dtype == Q3T_BOOL ? 1 : 2;
-        if (a->mask_stride_t != 1 || a->mask_stride_b < 0 || !aligned(a->mask, 4)) return false;
-        if (((a->batch - 1) * a->mask_stride_b + a->ctx) * es + 3 > (int64_t)INT32_MAX) return false;
-    }
-    return true;
+// A mask on the bundled grid: unit key stride, 4-byte aligned, its words addressed by 32-bit
+// byte offsets.
+static bool bundle_mask_ok(const q3t_decode_args *a) {
+    if (!a->mask) return true;
+    const int64_t es = a->mask_dtype == Q3T_F32 ? 4 : a->mask_dtype == Q3T_BOOL ? 1 : 2;
+    if (a->mask_stride_t != 1 || a->mask_stride_b < 0 || !aligned(a->mask, 4)) return false;
+    return ((a->batch - 1) * a->mask_stride_b + a->ctx) * es + 3 <= (int64_t)INT32_MAX;
 }
 static bool bundle_ok(const q3t_decode_args *a) {
-    return a->dtype == Q3T_BF16 && a->head_dim == 128 && a->query_len == 1 && (!a->mask || shares_ok(a)) &&
+    return a->dtype == Q3T_BF16 && a->head_dim == 128 && a->query_len == 1 && bundle_mask_ok(a) &&
            a->batch <= kBundleMaxBatch && a->q_heads / a->kv_heads <= 4;
 }
 static int decode_grid(const q3t_decode_args *a) {
@@ -1375,7 +1413,6 @@ static int64_t balanced_splits(const q3t_decode_args *a) {
 // Bundled grid: bundles (workgroups) per KV head, one workgroup per CU in all, and at most
 // kBundleMaxSeg requests per bundle.
 static int64_t bundle_count(const q3t_decode_args *a) {
-    if (a->mask) return shares_bundle_count(a->batch, a->kv_heads);
     const int64_t m = (kBundleGroups + a->kv_heads - 1) / a->kv_heads;
     const int64_t least = (a->batch + kBundleMaxSeg - 1) / kBundleMaxSeg;
     return m < least ? least : m;
@@ -1389,9 +1426,7 @@ static int64_t partial_floats(const q3t_decode_args *a) {
         case Q3T_GRID_CHUNKED:
             units = a->batch * a->kv_heads * chunk_count(a->batch, a->kv_heads, a->ctx, a->max_chunks);
             break;
-        case Q3T_GRID_BUNDLED:  // the shares grid publishes the states of requests cut between shares
-            return a->mask && shares_ok(a) ? shares_partial_floats(a->batch, a->kv_heads, a->q_heads / a->kv_heads) : 0;
-        default: break;
+        default: break;  // bundled: whole requests, no partial states
     }
     return units * R * (a->head_dim + 2);
 }
@@ -1438,28 +1473,32 @@ static void launch_split(const DecodeParams &p, hipStream_t s) {
         hipLaunchKernelGGL((decode_chunks_kernel<T, D, G, SQ, FUSE, M, false>), grid, dim3(kThreads), 0, s, p);
 }
 
+template <int G, bool F, int M>
+static void launch_bundled(const DecodeParams &p, hipStream_t s) {
+    // whole requests per workgroup, bundled by the step's plan when the call brings one
+    const int32_t *rank = p.plan;
+    const dim3 grid((uint32_t)p.bundles * p.Hkv);
+    if (F && (p.qnw || p.knw)) {
+        if constexpr (F) {
+            if (p.stream) hipLaunchKernelGGL((decode_bundled_kernel<G, F, true, true, M>), grid, dim3(kThreads), 0, s, rank, p.B, p.Hkv, p.bundles, p);
+            else hipLaunchKernelGGL((decode_bundled_kernel<G, F, false, true, M>), grid, dim3(kThreads), 0, s, rank, p.B, p.Hkv, p.bundles, p);
+        }
+    } else if (p.stream) {
+        hipLaunchKernelGGL((decode_bundled_kernel<G, F, true, false, M>), grid, dim3(kThreads), 0, s, rank, p.B, p.Hkv, p.bundles, p);
+    } else {
+        hipLaunchKernelGGL((decode_bundled_kernel<G, F, false, false, M>), grid, dim3(kThreads), 0, s, rank, p.B, p.Hkv, p.bundles, p);
+    }
+}
+
 template <typename T, int D, int G, int SQ, bool F, bool M>
 static void launch_decode(const DecodeParams &p, hipStream_t s) {
-    if constexpr (sizeof(T) == 2 && D == 128 && SQ == 1 && M && G <= 4) {
-        if (p.bundles > 0 && p.plan) {  // a mask: the shares grid
-            shares_launch(p, G, F, F && (p.qnw || p.knw), M, s);
-            return;
-        }
-    }
-    if constexpr (sizeof(T) == 2 && D == 128 && SQ == 1 && !M && G <= 4) {
+    if constexpr (sizeof(T) == 2 && D == 128 && SQ == 1 && G <= 4) {
         if (p.bundles > 0) {
-            // whole requests per workgroup; with the step's plan, its ranking section
-            const int32_t *rank = p.plan ? p.plan + shares_rank_offset(p.B, p.Hkv) : nullptr;
-            const dim3 grid((uint32_t)p.bundles * p.Hkv);
-            if (F && (p.qnw || p.knw)) {
-                if constexpr (F) {
-                    if (p.stream) hipLaunchKernelGGL((decode_bundled_kernel<G, F, true, true>), grid, dim3(kThreads), 0, s, rank, p.B, p.Hkv, p.bundles, p);
-                    else hipLaunchKernelGGL((decode_bundled_kernel<G, F, false, true>), grid, dim3(kThreads), 0, s, rank, p.B, p.Hkv, p.bundles, p);
-                }
-            } else if (p.stream) {
-                hipLaunchKernelGGL((decode_bundled_kernel<G, F, true, false>), grid, dim3(kThreads), 0, s, rank, p.B, p.Hkv, p.bundles, p);
+            if constexpr (M) {
+                if (p.mask_dtype == Q3T_BF16) launch_bundled<G, F, 1>(p, s);
+                else launch_bundled<G, F, 2>(p, s);
             } else {
-                hipLaunchKernelGGL((decode_bundled_kernel<G, F, false, false>), grid, dim3(kThreads), 0, s, rank, p.B, p.Hkv, p.bundles, p);
+                launch_bundled<G, F, 0>(p, s);
             }
             return;
         }
@@ -1683,13 +1722,12 @@ extern "C" int q3t_decode_attention(const q3t_decode_args *a, void *stream) {
 
 static bool plan_shape_ok(int64_t batch, int64_t ctx, int64_t q_heads, int64_t kv_heads) {
     return batch >= 0 && batch <= kBundleMaxBatch && ctx >= 1 && ctx <= (1 << 20) && kv_heads >= 1 &&
-           q_heads >= kv_heads && q_heads % kv_heads == 0 &&
-           (q_heads / kv_heads == 1 || q_heads / kv_heads == 2 || q_heads / kv_heads == 4);
+           q_heads >= kv_heads && q_heads % kv_heads == 0 && q_heads / kv_heads <= 4;
 }
 
 extern "C" int64_t q3t_decode_plan_bytes(int64_t batch, int64_t q_heads, int64_t kv_heads) {
     if (!plan_shape_ok(batch, 1, q_heads, kv_heads)) return -1;
-    return shares_plan_ints(batch, kv_heads) * 4;
+    return plan_ints(batch, kv_heads) * 4;
 }
 
 extern "C" int q3t_decode_plan(const int64_t *positions, int64_t batch, int64_t ctx, int64_t q_heads,
@@ -1697,6 +1735,6 @@ extern "C" int q3t_decode_plan(const int64_t *positions, int64_t batch, int64_t 
     if (!plan_shape_ok(batch, ctx, q_heads, kv_heads)) return Q3T_EINVAL;
     if (batch == 0) return Q3T_OK;
     if (!positions || !plan || !aligned(positions, 8) || !aligned(plan, 16)) return Q3T_EINVAL;
-    return shares_plan_launch(positions, (int)batch, (int)ctx, (int)shares_bundle_count(batch, kv_heads),
-                              shares_slot_cap(q_heads / kv_heads), plan, (hipStream_t)stream);
+    return plan_launch(positions, (int)batch, (int)ctx, (int)plan_bundle_count(batch, kv_heads), plan,
+                       (hipStream_t)stream);
 }

@@ -1,6 +1,6 @@
-// The parameter block of the decode attention launches (every grid's kernels take it by value)
-// and the helpers for its optional SDPA-style mask.  Shared by decode_attention.hip (the
-// chunked, balanced and bundled grids) and decode_shares.hip (the shares grid).
+// The parameter block of the decode attention launches (every grid's kernels take it by value),
+// the helpers for its optional SDPA-style mask, and the step plan's entry points
+// (decode_plan.hip).
 #pragma once
 
 #include "q3t_common.hpp"
@@ -33,19 +33,31 @@ struct DecodeParams {
     float eps;
     int stream;             // read K/V rows with the non-temporal cache policy (host choice)
     int64_t nk_ss, nv_ss, cs_ss;  // fused, two tokens: token strides of new K/V and cos/sin
-    const int32_t *plan;    // bundled grid: the step's plan (decode_shares.hip), null without one
+    const int32_t *plan;    // bundled grid: the step's plan (decode_plan.hip), null without one
 };
 
-// The shares grid (decode_shares.hip): shares per KV head, segment columns per share, plan
-// size, published-state floats and flag counters of a launch shape; the launch itself.
-int64_t shares_bundle_count(int64_t batch, int64_t kv_heads);
-int shares_slot_cap(int64_t group);
-int64_t shares_plan_ints(int64_t batch, int64_t kv_heads);
-int64_t shares_rank_offset(int64_t batch, int64_t kv_heads);  // ints before the ranking section
-int64_t shares_partial_floats(int64_t batch, int64_t kv_heads, int64_t group);
-int64_t shares_flag_count(int64_t batch, int64_t kv_heads);
-int shares_launch(const DecodeParams &p, int group, bool fused, bool norm, bool mask, hipStream_t s);
-int shares_plan_launch(const int64_t *pos, int batch, int ctx, int bundles, int cap, int32_t *plan, hipStream_t s);
+// The step plan (decode_plan.hip): bundles per KV head, plan size in int32 and its launch.
+int64_t plan_bundle_count(int64_t batch, int64_t kv_heads);
+int64_t plan_ints(int64_t batch, int64_t kv_heads);
+int plan_launch(const int64_t *pos, int batch, int ctx, int bundles, int32_t *plan, hipStream_t s);
+
+// 4 bytes per lane from global memory into LDS at lds_base + 4 * lane (the mask words of a
+// stage's rows); offsets past the resource's range write zeros.
+Q3T_DEVICE void load_to_lds4(i32x4_t rsrc, uint32_t voffset, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\t" Q3T_VMEM_SGPR_WAIT "buffer_load_dword %1, %2, 0 offen lds"
+                 :: "s"(lds_base), "v"(voffset), "s"(rsrc) : "memory", "m0");
+}
+
+// A mask term (log2 units) from the 4-byte word holding it; `sub` = its byte offset in the word.
+Q3T_DEVICE float mask_term(uint32_t word, uint32_t sub, int dtype) {
+    const uint32_t x = word >> (8 * sub);
+    switch (dtype) {
+        case Q3T_BF16: return bf16_to_float(x & 0xffffu) * 1.4426950408889634f;
+        case Q3T_F16: return (float)__builtin_bit_cast(_Float16, (uint16_t)(x & 0xffffu)) * 1.4426950408889634f;
+        case Q3T_F32: return __uint_as_float(word) * 1.4426950408889634f;
+        default: return (x & 0xffu) ? 0.0f : -INFINITY;  // bool: True attends
+    }
+}
 
 Q3T_DEVICE int mask_elem_size(int dtype) { return dtype == Q3T_F32 ? 4 : dtype == Q3T_BOOL ? 1 : 2; }
 

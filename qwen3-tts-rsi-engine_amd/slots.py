@@ -139,8 +139,8 @@ class SlotCache(Cache):
     def prepare(self):
         """Per-step hook, run after the positions change and before the layers (SlotGraph.compute
         does).  The reference rebuilds its scatter indices from the positions here
-        (continuous.py:147-150); the HIP writer reads the positions directly, and this cuts the
-        step's keys into the bundled grid's equal shares once for all the step's layers
+        (continuous.py:147-150); the HIP writer reads the positions directly, and this ranks and
+        bundles the step's requests for the bundled grid once for all the step's layers
         (``decode_plan``).  The plan buffer is allocated on the first call (SlotGraph's eager
         pass, before capture) and refilled by a kernel after."""
         positions = self.positions

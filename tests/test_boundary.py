@@ -85,20 +85,19 @@ def test_rejected_calls_return_negative_status_without_a_gpu(pkg):
     assert lib.q3t_decode_plan(16, 129, 1024, 16, 8, 16, None) == -1      # more requests than a plan covers
     assert lib.q3t_decode_plan(16, 4, 0, 16, 8, 16, None) == -1           # no arena rows
     assert lib.q3t_decode_plan(16, 4, (1 << 20) + 1, 16, 8, 16, None) == -1
-    assert lib.q3t_decode_plan(16, 4, 1024, 24, 8, 16, None) == -1        # 3 query heads per KV head
+    assert lib.q3t_decode_plan(16, 4, 1024, 40, 8, 16, None) == -1        # 5 query heads per KV head
     assert lib.q3t_decode_plan(16, 4, 1024, 16, 8, 8, None) == -1         # plan not 16-byte aligned
     assert lib.q3t_decode_plan(None, 0, 1024, 16, 8, None, None) == 0     # an empty batch launches nothing
-    # the plan's size: M = 32 shares per KV head of 8 (one workgroup per CU) and a header row,
-    # 8 entries of 16 bytes each (more shares when a batch needs more than 4 requests per
-    # share), then the bundle section: (batch, 0) and four (b, L) pairs of 4-byte ints for
-    # each of the M bundles
-    def size(shares):
-        return (shares + 1) * 8 * 16 + 8 + shares * 4 * 8
+    # the plan's size: (batch, M) and four (b, L) pairs of 4-byte ints for each of the M
+    # bundles of a KV head: M = 32 for 8 KV heads (one workgroup per CU), more when a batch
+    # needs more than 4 requests per bundle
+    def size(bundles):
+        return 8 + bundles * 4 * 8
     assert lib.q3t_decode_plan_bytes(64, 16, 8) == size(32)
     assert lib.q3t_decode_plan_bytes(128, 16, 16) == size(32)
     assert lib.q3t_decode_plan_bytes(128, 64, 64) == size(32)
     assert lib.q3t_decode_plan_bytes(128, 4, 4) == size(64)
-    assert lib.q3t_decode_plan_bytes(64, 24, 8) == -1
+    assert lib.q3t_decode_plan_bytes(64, 40, 8) == -1
     # the allocation-free entry point refuses, before touching any device, a call whose split
     # states would not fit its fixed 8 MiB array (1024 requests x 8 heads x 16 chunks)
     big = pkg._lib.DecodeArgs()
@@ -153,8 +152,8 @@ def test_decode_workspace_sizes(pkg):
 
 def test_decode_grid_choice(pkg):
     """The library's grid choice, without a GPU: the talker step (64 requests, 1024-row arena)
-    runs bundled, also with the reference's mask when it brings the step's plan, long arenas
-    balanced, short ones and small batches chunked; splits still selects balanced (> 0) or
+    runs bundled, also with the reference's mask, long arenas balanced, short ones and small
+    batches chunked; splits still selects balanced (> 0) or
     chunked (< 0) under the automatic choice."""
     decode_grid_for = pkg.decode_grid_for
     assert decode_grid_for(64, 1, 16, 8, 128, 1024) == "bundled"
@@ -164,7 +163,6 @@ def test_decode_grid_choice(pkg):
     assert decode_grid_for(32, 1, 16, 8, 128, 1024) == "chunked"
     assert decode_grid_for(64, 2, 16, 8, 128, 1024) == "chunked"
     assert decode_grid_for(64, 1, 16, 8, 128, 1024, masked=True) == "bundled"
-    assert decode_grid_for(64, 1, 16, 8, 128, 1024, masked=True, planned=False) == "chunked"
     assert decode_grid_for(64, 1, 16, 8, 128, 1024, torch.float32) == "chunked"
     assert decode_grid_for(64, 1, 16, 8, 128, 1024, splits=-1) == "chunked"
     assert decode_grid_for(64, 1, 16, 8, 128, 1024, splits=9) == "balanced"

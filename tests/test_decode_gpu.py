@@ -145,10 +145,9 @@ def test_bundled_grid_edges(pkg, device, group, batch, capacity, fused):
     expected = oatt.decode_attention(query[idx], keys[idx], values[idx], contexts.numpy()[idx], D ** -0.5)
     assert_attention_close(got[idx], expected)
     # the same launch from the step's plan: each request is still scored whole by one
-    # workgroup in the same order, so the outputs are bit-identical; and masked by SlotGraph.compute's mask (0 up to each
-    # position, the most negative bf16 after), the plan's equal shares of each head's keys
-    # (requests cut between shares merged through the workspace): the same arena rows,
-    # outputs in the bar
+    # workgroup in the same order, so the outputs are bit-identical; and masked by
+    # SlotGraph.compute's mask (0 up to each position, the most negative bf16 after): the same
+    # arena rows, outputs in the bar
     plan = pkg.decode_plan(positions, capacity, q_heads, kv_heads)
     allowed = torch.arange(capacity, device=device)[None, :] <= positions[:, None]
     mask = torch.where(allowed, 0.0, torch.finfo(torch.bfloat16).min).to(torch.bfloat16)[:, None, None, :]
@@ -168,119 +167,71 @@ def test_bundled_grid_edges(pkg, device, group, batch, capacity, fused):
     assert_attention_close(got[idx], expected)
 
 
-SLOTS, LAST, MERGE, PUBLISH = 8, 1, 2, 4
 PER_BUNDLE = 4
 
 
 def plan_parts(plan):
-    """Views of a plan tensor: the shares' segment entries (M, 8, 4), the 32-int header and
-    the bundle section (1 + 4 M, 2): (batch, 0), then four (b, L) pairs per bundle."""
-    shares = (plan.numel() - 2 - SLOTS * 4) // (SLOTS * 4 + 2 * PER_BUNDLE)
-    entries = plan[:shares * SLOTS * 4].view(shares, SLOTS, 4)
-    header = plan[shares * SLOTS * 4:(shares + 1) * SLOTS * 4]
-    bundles = plan[(shares + 1) * SLOTS * 4:].view(1 + PER_BUNDLE * shares, 2)
-    return entries, header, bundles
+    """Views of a plan tensor: its header (batch, M) and its table (M, 4, 2): four (request,
+    length) pairs for each of the M bundles (workgroups) of a KV head."""
+    return plan[:2], plan[2:].view(-1, PER_BUNDLE, 2)
 
 
-def check_plan(plan, contexts, capacity, q_heads, kv_heads):
-    """The plan's contract: a header (batch, shares, segment cap, capacity, zero-length mask);
-    every key of every request in exactly one segment; entries a prefix of each share's 8
-    slots, at most 16 / group of them; a request cut between shares has its earlier parts in
-    the first slot of the shares before (published) and its last part in the last slot of its
-    final share (merging them); and, unless it fell back to whole requests, shares of whole
-    64-key stages within one stage of each other, the last one excepted.  The bundle section
-    lists every request of the batch once, with its length, in at most four slots per bundle
-    ((-1, 0) elsewhere), and no bundle holds more keys than pairing the i-th longest request
-    with the i-th shortest gives.  Returns (fell back, stages per share)."""
-    entries, header, bundles = (t.cpu().numpy() for t in plan_parts(plan))
-    e = entries
-    shares = e.shape[0]
+def check_plan(plan, contexts, capacity, kv_heads):
+    """The plan's contract: the header (batch, M) with M = max(ceil(256 / kv_heads),
+    ceil(batch / 4)); every request of the batch listed once, with its length L = pos + 1
+    (0 for a position outside the arena), (-1, 0) in unused slots; bundle m holding the
+    requests of length ranks m, 2M-1-m, 2M+m, 4M-1-m, ranked longest first with ties by index
+    (checked against a sort done here).  Returns the keys of each bundle."""
+    header, table = (t.cpu().numpy() for t in plan_parts(plan))
     batch = len(contexts)
+    bundles = max(-(-256 // kv_heads), -(-batch // PER_BUNDLE))
+    assert list(header) == [batch, bundles] and table.shape == (bundles, PER_BUNDLE, 2)
     lengths = np.where((contexts >= 0) & (contexts < capacity), contexts + 1, 0)
-    cap = min(SLOTS, 16 // (q_heads // kv_heads))
-    assert list(header[:4]) == [batch, shares, cap, capacity] and not header[8:].any()
-    zero = sum(1 << b for b in range(batch) if lengths[b] == 0)
-    assert sum(int(np.uint32(header[4 + w])) << (32 * w) for w in range(4)) == zero
-    assert list(bundles[0]) == [batch, 0]
-    table = bundles[1:].reshape(-1, PER_BUNDLE, 2)
-    listed = sorted(int(b) for b in table[:, :, 0].reshape(-1) if b >= 0)
-    assert listed == list(range(batch))
-    assert all(table[m, k, 1] == lengths[table[m, k, 0]] for m, k in zip(*np.nonzero(table[:, :, 0] >= 0)))
-    assert ((table[:, :, 0] >= 0) | (table[:, :, 1] == 0)).all()
     order = sorted(range(batch), key=lambda b: (-lengths[b], b))
-    bundles_m = table.shape[0]
-    paired = [sum(lengths[order[r]] for r in (m, 2 * bundles_m - 1 - m, 2 * bundles_m + m, 4 * bundles_m - 1 - m)
-                  if r < batch) for m in range(bundles_m)]
-    assert table[:, :, 1].sum(1).max() <= max(paired)
-    covered = [np.zeros(n, int) for n in lengths]
-    keys, whole = [], True
-    for m in range(shares):
-        slots = e[m]
-        live = slots[:, 0] >= 0
-        n = int(live.sum())
-        assert live[:n].all() and n <= cap
-        total = 0
-        for k in range(n):
-            b, j0, j1, info = slots[k]
-            assert 0 <= b < batch and 0 <= j0 < j1 <= lengths[b]
-            covered[b][j0:j1] += 1
-            total += j1 - j0
-            assert bool(info & LAST) == (j1 == lengths[b])
-            whole = whole and j0 == 0 and j1 == lengths[b]
-            assert bool(info & PUBLISH) == (j1 < lengths[b])
-            if info & PUBLISH:
-                assert k == 0
-            assert bool(info & MERGE) == (j0 > 0 and j1 == lengths[b])
-            if info & MERGE:
-                assert k == n - 1
-                for i in range(1, (info >> 4) + 1):
-                    assert e[m - i][0][0] == b and e[m - i][0][3] & PUBLISH
-        keys.append(total)
-    assert all((c == 1).all() for c in covered)
-    stages = [(n + 63) // 64 for n in keys]
-    if not whole:
-        body = stages[:-1]
-        assert max(body) - min(body) <= 1 and stages[-1] <= max(body)
-    return whole, stages
+    for m in range(bundles):
+        for k, r in enumerate((m, 2 * bundles - 1 - m, 2 * bundles + m, 4 * bundles - 1 - m)):
+            want = (order[r], lengths[order[r]]) if r < batch else (-1, 0)
+            assert tuple(table[m, k]) == want, (m, k)
+    return table[:, :, 1].sum(1)
 
 
 @pytest.mark.parametrize("batch,capacity,group", [(1, 1024, 2), (6, 1024, 2), (64, 1024, 2), (100, 2048, 1),
-                                                  (128, 1024, 4), (16, 4096, 2)])
-def test_decode_plan_cuts_equal_shares(pkg, device, batch, capacity, group):
-    """The step's plan on the device: ties, invalid positions (negative, at or past the
-    capacity: no keys, listed in the header's mask) and, for 16 requests over 4096 rows,
-    requests spanning more than three shares (whole requests instead)."""
+                                                  (128, 1024, 4), (16, 4096, 3)])
+def test_decode_plan_pairs_longest_with_shortest(pkg, device, batch, capacity, group):
+    """The step's plan on the device: ties (a third of the requests share one length),
+    invalid positions (negative, at or past the capacity: length 0), more requests than
+    bundles (128 requests over 4 KV heads: four per bundle) and fewer (one request)."""
     gen = torch.Generator().manual_seed(900 + batch)
     contexts = torch.randint(-2, capacity + 2, (batch,), generator=gen)
     contexts[: batch // 3] = contexts[0]
     kv_heads = 8 if group < 4 else 4
     plan = pkg.decode_plan(contexts.to(device), capacity, kv_heads * group, kv_heads)
     assert tuple(plan.shape) == pkg.plan_shape(batch, kv_heads * group, kv_heads) and plan.dtype == torch.int32
-    check_plan(plan, contexts.numpy(), capacity, kv_heads * group, kv_heads)
+    check_plan(plan, contexts.numpy(), capacity, kv_heads)
     with pytest.raises(ValueError):
         pkg.decode_plan(torch.zeros(129, dtype=torch.int64, device=device), capacity, 16, 8)
     with pytest.raises(ValueError):
-        pkg.decode_plan(contexts.to(device), capacity, 24, 8)
+        pkg.decode_plan(contexts.to(device), capacity, 40, 8)   # 5 query heads per KV head
 
 
 def test_decode_plan_of_the_talker_step(pkg, device):
-    """The headline step's plan: 32 shares per head, all of 16 stages but one of 17 (the
-    seed-0 draw has 32,782 keys per head, 513 stages), no fallback."""
+    """The headline step's plan: 32 bundles per head of two requests each, 936 to 1099 keys
+    for a mean of 1024 (the seed-0 draw: 32,782 keys per head)."""
     contexts, *_ = _config2(device)
     plan = pkg.decode_plan(contexts.to(device), 1024, HQ, HKV)
-    whole, stages = check_plan(plan, contexts.numpy(), 1024, HQ, HKV)
-    assert not whole and sorted(stages) == [16] * 31 + [17]
+    keys = check_plan(plan, contexts.numpy(), 1024, HKV)
+    assert keys.sum() == 32782 and (plan_parts(plan)[1][:, 2:, 0] == -1).all().item()
+    assert keys.min() == 936 and keys.max() == 1099
 
 
 @pytest.mark.parametrize("masked", [False, True])
 def test_decode_plan_of_other_positions_stays_in_bounds(pkg, device, masked):
     """A plan is only valid for the positions it was made from.  A stale one (made for other
-    positions) or a malformed one (entries naming no request, key ranges past the arena)
-    gives other outputs but touches nothing outside the arguments: the fused step writes the
-    new K/V rows at the rows the plan names (the last key of each request it lists) and
-    nowhere else, and the output rows of requests it does not name stay as they were.  A plan
-    of another batch gives NaN rows masked; unmasked it is not used (the launch ranks the
-    requests itself)."""
+    positions) or a malformed one (entries naming no request, lengths past the arena) gives
+    other outputs but touches nothing outside the arguments: the fused step writes the new
+    K/V rows at the rows the plan names (the last key of each request it lists) and nowhere
+    else, and the output rows of requests it does not name stay as they were.  A plan of
+    another batch is not used (the launch ranks the requests itself)."""
     contexts, k, v, q, kn, vn = _config2(device, seed=13)
     positions = contexts.to(device)
     cos, sin = pkg.rope_tables(positions, D)
@@ -297,39 +248,29 @@ def test_decode_plan_of_other_positions_stays_in_bounds(pkg, device, masked):
     allowed = {(b, h, int(stale_ctx[b])) for b in range(64) for h in range(HKV)}
     assert changed.shape[0] > 0 and {tuple(int(x) for x in r) for r in changed} <= allowed
     bad = stale.clone()
-    entries, _, bundles = plan_parts(bad)
-    if masked:
-        entries[::3, 0, 0] = 1000     # no such request: the share lists nothing
-        entries[1::3, 0, 2] = 5000    # more keys than the arena has: clamped
-        named = set(int(b) for b in entries[:, :, 0].reshape(-1).cpu().tolist() if 0 <= b < 64)
-    else:
-        bundles[1::3, 0] = 1000       # no such request: the slot attends nothing
-        bundles[2::3, 1] = 5000       # more keys than the arena has: clamped
-        named = set(int(b) for b in bundles[1:, 0].cpu().tolist() if 0 <= b < 64)
+    table = plan_parts(bad)[1].view(-1, 2)
+    table[::3, 0] = 1000       # no such request: the slot attends nothing
+    table[1::3, 1] = 5000      # more keys than the arena has: clamped
+    named = set(int(b) for b in table[:, 0].cpu().tolist() if 0 <= b < 64)
     out = torch.full((64, 1, HQ, D), 7.0, device=device, dtype=torch.bfloat16)
     pkg.decode_attention(q, k, v, positions, grid="bundled", plan=bad, out=out, mask=mask)
     torch.cuda.synchronize()
-    assert masked or len(named) < 64
+    assert len(named) < 64
     for b in range(64):
         if b not in named:
             assert torch.all(out[b] == 7.0)
-    # a plan edited by hand can list a request's later part without its first one, whose
-    # share would have consumed the later part's published state: re-zero the workspace
-    pkg.reset_workspaces(device)
     other = pkg.decode_plan(positions[:60], 1024, HQ, HKV)  # 60 requests: the same plan shape
     out = pkg.decode_attention(q, k, v, positions, grid="bundled", plan=other, mask=mask)
-    if masked:
-        assert torch.isnan(out.float()).all()
-    else:
-        assert torch.equal(out, pkg.decode_attention(q, k, v, positions, grid="bundled"))
+    assert torch.equal(out, pkg.decode_attention(q, k, v, positions, grid="bundled", mask=mask))
     with pytest.raises(ValueError):
         pkg.decode_attention(q, k, v, positions, grid="bundled", plan=stale[:10], mask=mask)
 
 
 def test_bundled_grid_is_deterministic_and_refuses_what_it_cannot_run(pkg, device):
-    """Repeated launches are bit-identical, with and without the step's plan; asked for by
-    name, the grid refuses a mask without a plan, two query tokens and fp32 rows (the
-    automatic choice runs them on another grid)."""
+    """Repeated launches are bit-identical, with and without the step's plan and a mask (a
+    bool mask of the positions' own range gives the unmasked result bit for bit); asked for
+    by name, the grid refuses a mask without unit key stride, two query tokens and fp32 rows
+    (the automatic choice runs them on another grid)."""
     contexts, k, v, q, _, _ = _config2(device, seed=12)
     positions = contexts.to(device)
     first = pkg.decode_attention(q, k, v, positions, grid="bundled").clone()
@@ -345,8 +286,10 @@ def test_bundled_grid_is_deterministic_and_refuses_what_it_cannot_run(pkg, devic
         assert torch.equal(pkg.decode_attention(q, k, v, positions, grid="bundled", plan=plan, mask=mask), planned)
     assert_attention_close(f64(planned), expected)
     keep = torch.arange(1024, device=device)[None, None, None, :] <= positions[:, None, None, None]
+    assert torch.equal(pkg.decode_attention(q, k, v, positions, mask=keep, grid="bundled"), first)
+    wide = torch.arange(2048, device=device)[None, None, None, :] <= 2 * positions[:, None, None, None]
     with pytest.raises(ValueError, match="unsupported"):
-        pkg.decode_attention(q, k, v, positions, mask=keep, grid="bundled")
+        pkg.decode_attention(q, k, v, positions, mask=wide[..., ::2], grid="bundled")
     with pytest.raises(ValueError, match="unsupported"):
         pkg.decode_attention(q.float(), k.float(), v.float(), positions, grid="bundled")
     with pytest.raises(ValueError, match="unsupported"):

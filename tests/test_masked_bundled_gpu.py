@@ -1,6 +1,6 @@
-"""The bundled grid's masked launches, which run on the step's plan (equal shares of each KV
-head's keys, every request of a share scored as its own MFMA columns, requests cut between
-shares merged through the workspace), against the float64 oracle.
+"""The bundled grid's masked launches against the float64 oracle: whole requests per
+workgroup, each stage's mask words loaded with its K/V rows and added to the scores of keys
+0 ... pos[b] (bf16 masks on a branch-free path, bool, fp16 and fp32 masks on the general one).
 
 The reference's masked talker flow is covered at full size: SlotGraph.compute builds the
 (B, 1, 1, ctx) mask 0 / finfo.min for keys j <= pos[b] every step and hands it to every layer
@@ -15,7 +15,6 @@ from oracle import bf16 as obf16
 from oracle import kv as okv
 from oracle import rope as orope
 from tests._util import assert_attention_close, bits, f64, from_bits
-from tests.test_decode_gpu import check_plan, plan_parts
 
 pytestmark = pytest.mark.gpu
 
@@ -56,9 +55,9 @@ def _slot_graph_mask(positions, width, dtype=torch.bfloat16):
 def test_reference_masked_talker_step_runs_on_the_bundled_grid(pkg, device, seed):
     """64 requests over a 1024-row arena, contexts U[64, 1024]: the fused step with the
     reference's per-step mask over the whole arena, on the bundled grid (the automatic choice
-    for the planned, masked call), matches the oracle; the arena rows are bit-exact."""
+    for the masked call), matches the oracle, with and without the step's plan; the arena rows
+    are bit-exact."""
     assert pkg.decode_grid_for(64, 1, HQ, HKV, D, 1024, masked=True) == "bundled"
-    assert pkg.decode_grid_for(64, 1, HQ, HKV, D, 1024, masked=True, planned=False) == "chunked"
     gen = torch.Generator().manual_seed(seed)
     contexts = torch.randint(64, 1025, (64,), generator=gen)
     k, v, q, kn, vn = _inputs(64, 1024, contexts, 100 + seed, device)
@@ -67,18 +66,23 @@ def test_reference_masked_talker_step_runs_on_the_bundled_grid(pkg, device, seed
     mask = _slot_graph_mask(positions, 1024)
     ek, ev, expected = _fused_oracle(k, v, q, kn, vn, contexts.numpy(), cos, sin)
     plan = pkg.decode_plan(positions, 1024, HQ, HKV)
+    k0, v0 = bits(k).copy(), bits(v).copy()
     out = pkg.decode_step(q, kn, vn, k, v, positions, cos, sin, mask=mask, plan=plan)
     assert np.array_equal(bits(k), ek) and np.array_equal(bits(v), ev)
     assert_attention_close(f64(out)[:, 0], expected[:, 0])
+    k2, v2 = from_bits(k0, device), from_bits(v0, device)
+    unplanned = pkg.decode_step(q, kn, vn, k2, v2, positions, cos, sin, mask=mask)
+    assert torch.equal(unplanned, out) and torch.equal(k2, k) and torch.equal(v2, v)
 
 
 @pytest.mark.parametrize("kind", ["bool", "additive_bf16", "additive_f16", "additive_f32"])
-@pytest.mark.parametrize("batch,group", [(64, 2), (128, 1), (96, 4)])
-def test_arbitrary_masks_on_the_bundled_grid(pkg, device, kind, batch, group):
+@pytest.mark.parametrize("batch,group,capacity", [(64, 2, 1024), (128, 1, 1024), (96, 4, 1024), (64, 2, 1023),
+                                                  (37, 1, 333)])
+def test_arbitrary_masks_on_the_bundled_grid(pkg, device, kind, batch, group, capacity):
     """Any additive or bool mask with unit key stride is added to the scores of keys
     0 ... pos[b] (SDPA's semantics within the positions' range), including finite additive
-    terms, on every request of a share and across the requests cut between shares."""
-    capacity = 1024
+    terms; odd mask rows (1023 and 333 keys) put a request's 2-byte terms at odd element
+    offsets, so the two halves of a mask word serve different keys."""
     kv_heads = HKV if group < 4 else 4
     gen = torch.Generator().manual_seed(200 + batch + group)
     contexts = torch.randint(0, capacity, (batch,), generator=gen)
@@ -96,49 +100,6 @@ def test_arbitrary_masks_on_the_bundled_grid(pkg, device, kind, batch, group):
     plan = pkg.decode_plan(positions, capacity, kv_heads * group, kv_heads)
     out = pkg.decode_attention(q, k, v, positions, mask=mask[:, None].to(device), plan=plan, grid="bundled")
     expected = oatt.decode_attention(f64(q), f64(k), f64(v), contexts.numpy(), D ** -0.5, mask=omask)
-    assert_attention_close(f64(out), expected)
-
-
-@pytest.mark.parametrize("fused", [False, True])
-def test_requests_cut_across_three_shares(pkg, device, fused):
-    """32 requests over 256 workgroups (32 shares per head): a few long requests among short
-    ones span three shares, so their final share merges two published parts."""
-    batch, capacity = 32, 2048
-    contexts = torch.full((batch,), 500)
-    contexts[[3, 11, 20]] = torch.tensor([1100, 1113, 1126])
-    plan_ctx = contexts.clone()
-    k, v, q, kn, vn = _inputs(batch, capacity, contexts, 400, device)
-    positions = contexts.to(device)
-    plan = pkg.decode_plan(positions, capacity, HQ, HKV)
-    whole, _ = check_plan(plan, plan_ctx.numpy(), capacity, HQ, HKV)
-    e = plan_parts(plan)[0].cpu().numpy()
-    assert not whole and ((e[:, :, 3] >> 4) == 2).any()   # some request spans three shares
-    mask = _slot_graph_mask(positions, capacity)
-    if fused:
-        cos, sin = pkg.rope_tables(positions, D)
-        ek, ev, expected = _fused_oracle(k, v, q, kn, vn, contexts.numpy(), cos, sin)
-        out = pkg.decode_step(q, kn, vn, k, v, positions, cos, sin, plan=plan, grid="bundled", mask=mask)
-        assert np.array_equal(bits(k), ek) and np.array_equal(bits(v), ev)
-    else:
-        expected = oatt.decode_attention(f64(q), f64(k), f64(v), contexts.numpy(), D ** -0.5)
-        out = pkg.decode_attention(q, k, v, positions, plan=plan, grid="bundled", mask=mask)
-    assert_attention_close(f64(out), expected)
-
-
-def test_whole_request_fallback(pkg, device):
-    """128 requests whose short ones cluster: a share would hold more requests than MFMA
-    columns, so the plan pairs whole requests longest with shortest instead; the launch
-    reads the same plan format."""
-    batch, capacity = 128, 1024
-    contexts = torch.full((batch,), 900)
-    contexts[40:100] = 3
-    k, v, q, _, _ = _inputs(batch, capacity, contexts, 500, device)
-    positions = contexts.to(device)
-    plan = pkg.decode_plan(positions, capacity, HQ, HKV)
-    whole, _ = check_plan(plan, contexts.numpy(), capacity, HQ, HKV)
-    assert whole
-    out = pkg.decode_attention(q, k, v, positions, plan=plan, grid="bundled", mask=_slot_graph_mask(positions, capacity))
-    expected = oatt.decode_attention(f64(q), f64(k), f64(v), contexts.numpy(), D ** -0.5)
     assert_attention_close(f64(out), expected)
 
 

@@ -226,7 +226,7 @@ def test_talker_step_on_the_bundled_grid_reads_the_step_plan(pkg, device):
         torch.cuda.synchronize()
         assert twin.cache.plan is None and graph.cache.plan is not None
         lengths = positions.numpy() + 1
-        table = plan_parts(graph.cache.plan)[2].cpu().numpy()[1:]
+        table = plan_parts(graph.cache.plan)[1].cpu().numpy().reshape(-1, 2)
         listed = table[table[:, 0] >= 0]
         np.testing.assert_array_equal(np.sort(listed[:, 0]), np.arange(batch))
         np.testing.assert_array_equal(listed[:, 1], lengths[listed[:, 0]])

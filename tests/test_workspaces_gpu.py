@@ -74,8 +74,7 @@ def _captured(pkg, grid, problem, out):
 def test_graphs_replay_in_any_order(pkg, device):
     """Two graphs of split launches captured one after the other and replayed second first,
     then alternately with their inputs rewritten in place between replays; a third graph
-    holds the masked bundled launch, whose requests cut between shares publish states and
-    flags through its workspace."""
+    holds a masked bundled launch with the step's plan."""
     a = _problem(64, 1024, 3, device)
     b = _problem(48, 2048, 4, device)
     out_a = torch.empty(64, 1, HQ, D, device=device, dtype=torch.bfloat16)
