@@ -1234,11 +1234,15 @@ __global__ void __launch_bounds__(kThreads) decode_bundled_kernel(const int32_t 
 #pragma unroll
             for (int i = 0; i < 4; ++i) x[i] = j0 + i < L ? st[i] * scale : -INFINITY;
         }
+        // a column's maximum over the stage is the largest of its four lanes' maxima, so a
+        // column passes the threshold exactly when one of its lanes does: the exchanges
+        // across the lanes run only when some lane passes (the first stage of a request and
+        // the rare rescale), off the chain of the other stages; the outputs are unchanged
         float mb = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-        mb = fmaxf(mb, xor16(mb));
-        mb = fmaxf(mb, xor32(mb));
-        const bool up = mb > mx + kRescaleLog2;
-        if (__builtin_amdgcn_ballot_w64(up)) {
+        if (__builtin_amdgcn_ballot_w64(mb > mx + kRescaleLog2)) {
+            mb = fmaxf(mb, xor16(mb));
+            mb = fmaxf(mb, xor32(mb));
+            const bool up = mb > mx + kRescaleLog2;
             const float mn = up ? mb : mx;
             const float alpha = fexp2(mx - mn);
             l *= alpha;
