@@ -177,9 +177,10 @@ typedef struct q3t_decode_args {
     int64_t nk_stride_b, nk_stride_h, nv_stride_b, nv_stride_h;
     const void *cos, *sin;
     int64_t cs_stride_b;
-    /* workspace: a fixed 256 KiB counter region (kv_heads * batch <= 65536), then the
-       partial states of split requests; zero-filled before first use, its counters left
-       zeroed by every launch.  Launches that overlap in time must not share one. */
+    /* workspace (chunked and balanced grids): a fixed 256 KiB counter region
+       (kv_heads * batch <= 65536), then the partial states of split requests; zero-filled
+       before first use, its counters left zeroed by every launch.  Launches that overlap in
+       time must not share one.  The bundled grid uses none (may be NULL). */
     void *workspace;
     int64_t workspace_bytes;
     int64_t max_chunks;      /* chunked grid: chunks per request and KV head, <= 1024; <= 0:
@@ -212,7 +213,8 @@ typedef struct q3t_decode_args {
 enum { Q3T_GRID_AUTO = 0, Q3T_GRID_CHUNKED = 1, Q3T_GRID_BALANCED = 2, Q3T_GRID_BUNDLED = 3 };
 
 /* Bytes of workspace q3t_decode_attention needs for this call (its sizes, `fused`, `mask`,
-   `max_chunks`, `splits` and `grid`; pointers are not read); -1 for malformed sizes.  No
+   `max_chunks`, `splits` and `grid`; pointers are not read), 0 on the bundled grid; -1 for
+   malformed sizes.  No
    counterpart in the reference (its attention operator allocates internally); callers size
    the buffer once, outside graph capture. */
 int64_t q3t_decode_workspace_bytes(const q3t_decode_args *args);

@@ -86,9 +86,10 @@ def _run_decode(args: _lib.DecodeArgs, device: torch.device, what: str, no_alloc
             need = lib.q3t_decode_workspace_bytes(args)
             if need < 0:
                 raise ValueError(f'{what}: invalid sizes')
-            ws = workspace(device, need, stream)
-            args.workspace = ws.data_ptr()
-            args.workspace_bytes = ws.numel()
+            if need > 0:  # the bundled grid needs none
+                ws = workspace(device, need, stream)
+                args.workspace = ws.data_ptr()
+                args.workspace_bytes = ws.numel()
             status = lib.q3t_decode_attention(args, stream)
     _lib.check(status, what)
 

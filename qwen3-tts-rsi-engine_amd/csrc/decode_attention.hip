@@ -1454,6 +1454,8 @@ extern "C" int q3t_decode_grid(const q3t_decode_args *a) {
 
 extern "C" int64_t q3t_decode_workspace_bytes(const q3t_decode_args *a) {
     if (!a || !decode_sizes_ok(a)) return -1;
+    // the bundled grid attends whole requests: no counters, no partial states
+    if (decode_grid(a) == Q3T_GRID_BUNDLED) return 0;
     return counters_bytes() + partial_floats(a) * 4;
 }
 
@@ -1720,7 +1722,8 @@ extern "C" int q3t_decode_attention(const q3t_decode_args *a, void *stream) {
     const int st = decode_params(a, (char *)a->workspace, p);
     if (st != Q3T_OK) return st;
     const int64_t need = q3t_decode_workspace_bytes(a);
-    if (!a->workspace || a->workspace_bytes < need || !aligned(a->workspace, 16)) return Q3T_EWORKSPACE;
+    if (need > 0 && (!a->workspace || a->workspace_bytes < need || !aligned(a->workspace, 16)))
+        return Q3T_EWORKSPACE;
     return decode_launch(a, p, stream);
 }
 

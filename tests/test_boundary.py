@@ -119,14 +119,14 @@ def test_decode_workspace_sizes(pkg):
     """256 KiB of counters, then one (G * query_len) x (head_dim + 2) fp32 state per part.
     Chunked grid: ctx 1024 is 16 blocks of 64 keys, chunks capped by max_chunks, by default
     at ceil(512 / (batch * kv_heads)).  Balanced grid: two state slots per workgroup, by
-    default 256 / kv_heads workgroups per head.  Bundled grid: no partial states.  Automatic
+    default 256 / kv_heads workgroups per head.  Bundled grid: no workspace at all.  Automatic
     choice: bundled for bf16 single-token launches of 64..128 requests (x 8 heads >= 512) over
     1024..2047 rows, balanced from 2048 rows, chunked otherwise."""
     lib = pkg.library()
     counters = 65536 * 4
     state = 2 * 130 * 4
-    assert _ws(lib, pkg, 64, 1, 1024) == counters                                    # bundled
-    assert _ws(lib, pkg, 128, 1, 2047) == counters                                   # bundled
+    assert _ws(lib, pkg, 64, 1, 1024) == 0                                           # bundled
+    assert _ws(lib, pkg, 128, 1, 2047) == 0                                          # bundled
     assert _ws(lib, pkg, 129, 1, 1024) == counters + 129 * 8 * 1 * state             # chunked
     assert _ws(lib, pkg, 63, 1, 1024) == counters + 63 * 8 * 2 * state               # chunked
     assert _ws(lib, pkg, 64, 1, 1023) == counters + 64 * 8 * 1 * state               # chunked
@@ -134,7 +134,7 @@ def test_decode_workspace_sizes(pkg):
     assert _ws(lib, pkg, 64, 1, 1024, masked=True) == counters + 64 * 8 * 1 * state  # mask: chunked
     assert _ws(lib, pkg, 64, 1, 1024, grid=1) == counters + 64 * 8 * 1 * state       # named chunked
     assert _ws(lib, pkg, 64, 1, 1024, grid=2) == counters + 8 * 32 * 2 * state       # named balanced
-    assert _ws(lib, pkg, 8, 1, 64, grid=3) == counters                               # named bundled
+    assert _ws(lib, pkg, 8, 1, 64, grid=3) == 0                                      # named bundled
     assert _ws(lib, pkg, 64, 2, 1024, grid=3) == counters  # sized; the launch refuses the grid
     assert _ws(lib, pkg, 64, 1, 1024, grid=4) == -1       # no such grid
     assert _ws(lib, pkg, 64, 1, 4096) == counters + 8 * 32 * 2 * state              # balanced
