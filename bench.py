@@ -85,15 +85,16 @@ def prefill_detail(pkg, device, reps=20):
     out = torch.empty(LAYERS, total, HQ, D, device=device, dtype=torch.bfloat16)
 
     def step(attention_only):
-        # prefill_step's kernels: the K/V prologue, then attention rotating the raw queries
+        # prefill_step's kernels: the key prologue, then attention rotating the raw queries,
+        # reading the values from the projection rows and copying them into the arena
         for layer in range(LAYERS):
             row = qkv[layer]
             q, k, v = row[:, :HQ], row[:, HQ:HQ + HKV], row[:, HQ + HKV:]
             if not attention_only:
-                pkg.prefill_rope_write(q, k, v, cos, sin, dcu, arena[layer], arena[LAYERS + layer],
+                pkg.prefill_rope_write(q, k, None, cos, sin, dcu, arena[layer], arena[LAYERS + layer],
                                        rotate_query=False)
             pkg.prefill_attention(q, arena[layer], arena[LAYERS + layer], dcu, longest,
-                                  out=out[layer], cos=cos, sin=sin)
+                                  out=out[layer], cos=cos, sin=sin, new_values=v)
 
     times = {}
     for attention_only in (False, True):

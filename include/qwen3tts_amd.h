@@ -282,7 +282,7 @@ int q3t_decode_reset_workspace(void *workspace, int64_t workspace_bytes, void *s
 typedef struct q3t_prefill_args {
     int64_t batch, total_tokens, max_seqlen, q_heads, kv_heads, head_dim;
     float scale;
-    const int32_t *cu_seqlens;     /* device (batch + 1) */
+    const int32_t *cu_seqlens;     /* device (batch + 1), non-decreasing */
     const void *query;             /* (tokens, q_heads, head_dim) bf16 */
     int64_t q_stride_t, q_stride_h;
     const void *keys, *values;     /* arena views */
@@ -305,6 +305,14 @@ typedef struct q3t_prefill_args {
        0 / -inf); 16-byte aligned rows */
     const void *mask;
     int64_t mask_dtype, mask_stride_b, mask_stride_q;
+    /* optional bf16 value rows (tokens, kv_heads, head_dim) of the step's tokens as the
+       projection wrote them (strides in elements, 16-byte aligned): the products read key
+       j's value of request b from token cu_seqlens[b] + j instead of `values`, and the
+       launch copies every token's row into `values` at its position (rows < capacity), the
+       value half of q3t_prefill_rope_write (which then runs with value == NULL).  Causal
+       launches only (mask == NULL): Q3T_EINVAL with a mask. */
+    const void *new_values;
+    int64_t nv_stride_t, nv_stride_h;
 } q3t_prefill_args;
 
 int q3t_prefill_attention(const q3t_prefill_args *args, void *stream);
@@ -314,7 +322,9 @@ int q3t_prefill_attention(const q3t_prefill_args *args, void *stream);
  * rows indexed by token) and the paired write of rotated keys and raw values into the
  * arena slot of each request.  q_out receives the rotated queries; with q_out == NULL only
  * the keys and values are handled (query and its strides are then ignored) and
- * q3t_prefill_attention rotates the queries itself from its cos/sin arguments.
+ * q3t_prefill_attention rotates the queries itself from its cos/sin arguments.  With
+ * value == NULL only the keys are written (value, its strides and arena_values are ignored):
+ * q3t_prefill_attention then copies the values (its new_values).
  * Replaces: the per-layer RoPE + DynamicCache fill of PrefillGraph.compute
  * (prefill_graph.py:38-43) and the later copy_packed_prefix into the arena
  * (continuous.py:468-469).

@@ -67,7 +67,7 @@ class PrefillArgs(ctypes.Structure):
         ("capacity", c_i64),
         ("cos", c_vp), ("sin", c_vp), ("cs_stride_t", c_i64),
         ("kv_lens", c_vp), ("mask", c_vp), ("mask_dtype", c_i64), ("mask_stride_b", c_i64),
-        ("mask_stride_q", c_i64),
+        ("mask_stride_q", c_i64), ("new_values", c_vp), ("nv_stride_t", c_i64), ("nv_stride_h", c_i64),
     ]
 
 

@@ -450,7 +450,7 @@ def attention(module, query, key, value, attention_mask, **kwargs):
 
 
 def prefill_attention(query, keys, values, cu_seqlens, max_seqlen, *, scale=None, kv_slots=None,
-                      out=None, cos=None, sin=None, kv_lens=None, mask=None):
+                      out=None, cos=None, sin=None, kv_lens=None, mask=None, new_values=None):
     """Varlen causal GQA: query (T, Hq, D) packed by cu_seqlens (B+1, int32); keys/values
     (slots, Hkv, capacity, D) arena views holding each request's keys at positions
     0 ... len-1 (slot b, or kv_slots[b]).  Returns (T, Hq, D).  With cos/sin (bf16 (T, D)
@@ -463,7 +463,12 @@ def prefill_attention(query, keys, values, cu_seqlens, max_seqlen, *, scale=None
     ``mask`` (B or 1, 1, len or 1, capacity): an SDPA-style mask (additive bf16 / fp16 /
     fp32, or bool with True = attend) over every key of the view; the causal rule is then
     off and the mask alone decides, as with the reference's explicit masks.  A query that
-    sees no key gets a zero row."""
+    sees no key gets a zero row.
+
+    ``new_values`` (T, Hkv, D) bf16: the step's value rows as the projection wrote them
+    (``prefill_rope_write(value=None)`` left them out of the arena): the products read them
+    and the same launch copies each into ``values`` at its token's position.  Not with
+    ``mask``."""
     if query.ndim != 3 or keys.ndim != 4 or values.shape != keys.shape:
         raise ValueError('expected (T, Hq, D) queries and arena key/value views')
     total, q_heads, head_dim = query.shape
@@ -515,6 +520,15 @@ def prefill_attention(query, keys, values, cu_seqlens, max_seqlen, *, scale=None
             raise ValueError('kv_lens must be an int32 (B,) tensor')
         _lib.require_gpu(query, kv_lens)
         a.kv_lens = kv_lens.data_ptr()
+    if new_values is not None:
+        if mask is not None:
+            raise ValueError('new_values needs the causal rule: not with an explicit mask')
+        if (new_values.ndim != 3 or tuple(new_values.shape) != (total, kv_heads, head_dim)
+                or new_values.dtype != torch.bfloat16 or new_values.stride(2) != 1):
+            raise ValueError(f'new_values must be bf16 ({total}, {kv_heads}, {head_dim}) token rows')
+        _lib.require_gpu(query, new_values)
+        a.new_values = new_values.data_ptr()
+        a.nv_stride_t, a.nv_stride_h = new_values.stride()[:2]
     if mask is not None:
         m = _prefill_mask(mask.to(device), batch, int(max_seqlen), keys.shape[2])
         a.mask = m.data_ptr()

@@ -92,15 +92,21 @@ __global__ void __launch_bounds__(256) prefill_rope_write_kernel(PrefillRopeWrit
             } else if (write_kv) {
                 const int h = hd - qh;
                 const char *krow = p.k + ((int64_t)t * p.k_st + h * p.k_sh) * 2;
-                const char *vrow = p.v + ((int64_t)t * p.v_st + h * p.v_sh) * 2;
                 U4 x1 = load16(krow + c * 16), x2 = load16(krow + (half + c * 8) * 2), y1, y2;
-                const U4 w1 = load16(vrow + c * 16), w2 = load16(vrow + (half + c * 8) * 2);
+                U4 w1 = {0u, 0u, 0u, 0u}, w2 = w1;
+                if (p.v) {  // without value rows the attention launch copies them
+                    const char *vrow = p.v + ((int64_t)t * p.v_st + h * p.v_sh) * 2;
+                    w1 = load16(vrow + c * 16);
+                    w2 = load16(vrow + (half + c * 8) * 2);
+                }
                 rope8(&x1.x, &x2.x, &c1.x, &c2.x, &s1.x, &s2.x, &y1.x, &y2.x);
                 const int64_t a = (slot * p.a_sb + h * p.a_sh + pos * p.a_st) * 2;
                 store16(p.ak + a + c * 16, y1);
                 store16(p.ak + a + (half + c * 8) * 2, y2);
-                store16(p.av + a + c * 16, w1);
-                store16(p.av + a + (half + c * 8) * 2, w2);
+                if (p.v) {
+                    store16(p.av + a + c * 16, w1);
+                    store16(p.av + a + (half + c * 8) * 2, w2);
+                }
             }
         }
     }
@@ -161,7 +167,76 @@ struct PrefillParams {
     const char *mask;     // optional (B, 1, Lq, capacity) additive mask: every key is scored
     int mdt;              // mask element type (Q3T_BF16, Q3T_F16 or Q3T_F32)
     int64_t m_sb, m_sq;   // mask strides (elements) of requests and query rows; keys unit-stride
+    // optional value rows of the step's tokens as the projection wrote them: the products
+    // read them (key j of request b is token cu[b] + j) and the workgroups past the
+    // attention grid copy them into the arena view `v` at each token's position
+    const char *nv;
+    int64_t nv_st, nv_sh;
+    int attn_wgs;         // workgroups of the attention grid (the copy workgroups follow)
 };
+
+constexpr int kCopyTokens = 16;  // value rows of 16 packed tokens per copy workgroup
+
+// Copy workgroup `unit`: for each group of 16 of its packed tokens, wave w copies the value
+// rows (every KV head) of tokens 4w ... 4w + 3 into the arena at their positions within their
+// requests (rows past the capacity are not stored), all of a group's loads issued before its
+// first store.
+template <int D>
+Q3T_DEVICE void copy_value_rows(const PrefillParams &p, int unit) {
+    constexpr int CPR = D / 8;  // 16-byte chunks per row
+    constexpr int PER = 8;      // chunks per lane in flight
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int start_l = 0x7fffffff;
+    int64_t slot_l = 0;
+    if (p.B <= 64 && lane < p.B) {
+        start_l = p.cu[lane];
+        slot_l = p.slots ? p.slots[lane] : lane;
+    }
+    const int chunks = p.Hkv * CPR;  // per token
+    for (int group = 0; group < kCopyTokens / 16; ++group) {
+        const int t0 = unit * kCopyTokens + group * 16 + 4 * wave;
+        if (t0 >= p.T) break;
+        // the four tokens' arena row offsets (elements), -1 for no row
+        int64_t row[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = t0 + j;
+            row[j] = -1;
+            if (t >= p.T) continue;
+            int start;
+            int64_t slot;
+            if (p.B <= 64) {
+                const int n = __builtin_popcountll(__builtin_amdgcn_ballot_w64(start_l <= t));
+                const int b = n > 0 ? n - 1 : 0;
+                start = __builtin_amdgcn_readlane(start_l, b);
+                slot = ((int64_t)__builtin_amdgcn_readlane((int)(slot_l >> 32), b) << 32) |
+                       (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)slot_l, b);
+            } else {
+                const int b = request_of(p.cu, p.B, t);
+                start = p.cu[b];
+                slot = p.slots ? p.slots[b] : b;
+            }
+            const int pos = t - start;
+            if (pos >= 0 && pos < p.cap) row[j] = slot * p.v_sb + (int64_t)pos * p.v_st;
+        }
+        for (int f0 = 0; f0 < 4 * chunks; f0 += 64 * PER) {
+            U4 buf[PER];
+            int64_t dst[PER];
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int f = f0 + 64 * i + lane, j = f / chunks, it = f % chunks;
+                const int hh = it / CPR, ch = it % CPR;
+                const int64_t r = j == 0 ? row[0] : j == 1 ? row[1] : j == 2 ? row[2] : j == 3 ? row[3] : -1;
+                dst[i] = r < 0 ? -1 : (r + hh * p.v_sh) * 2 + ch * 16;
+                buf[i] = dst[i] < 0 ? U4{0u, 0u, 0u, 0u}
+                                    : load16(p.nv + ((int64_t)(t0 + j) * p.nv_st + hh * p.nv_sh) * 2 + ch * 16);
+            }
+#pragma unroll
+            for (int i = 0; i < PER; ++i)
+                if (dst[i] >= 0) store16((char *)p.v + dst[i], buf[i]);
+        }
+    }
+}
 
 constexpr float kEmptyP = -1.0e30f;  // finite running maximum before any visible key (masked)
 
@@ -215,6 +290,10 @@ prefill_attention_kernel(PrefillParams p) {
 
     // the wave index through readfirstlane: wave-uniform for the compiler too, so that the
     // per-wave load resources stay in scalar registers
+    if ((int)blockIdx.x >= p.attn_wgs) {  // past the attention grid: value rows to copy
+        if constexpr (MB == 0) copy_value_rows<D>(p, (int)blockIdx.x - p.attn_wgs);
+        return;
+    }
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, c = lane & 15;
     const int hgroups = p.Hq / GH;
@@ -225,7 +304,7 @@ prefill_attention_kernel(PrefillParams p) {
     // Measured on the 16-prompt workload (seed 0): the most loaded CU from 27 to 20 tiles.
     const int wg = [&] {
         const int xcd = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
-        const int rounds = gridDim.x / (kXcds * kCusPerXcd);  // complete rounds on every XCD
+        const int rounds = p.attn_wgs / (kXcds * kCusPerXcd);  // complete rounds on every XCD
         if (j >= rounds * kCusPerXcd) return (int)blockIdx.x;
         const int r = j / kCusPerXcd, pos = j % kCusPerXcd;
         const bool flip = (r & 3) == 1 || (r & 3) == 2;
@@ -292,8 +371,10 @@ prefill_attention_kernel(PrefillParams p) {
     const int ntiles = kv_end > 0 ? (kv_end + kTile - 1) / kTile : 0;
     const int wq0 = q0 + 16 * wave;              // first query of this wave
     // keys [0, wave_end) can be visible to the wave; steps reaching past mask_from need the
-    // per-key rule (the diagonal or the end of the keys)
-    const int wave_end = MB ? kv_end : min(wq0 + 16, kv_end);
+    // per-key rule (the diagonal or the end of the keys).  A wave whose queries all lie past
+    // the request (the tail of its last block) scores nothing: it only loads its share of
+    // every tile and joins the barriers.
+    const int wave_end = wq0 >= n ? 0 : MB ? kv_end : min(wq0 + 16, kv_end);
     const int mask_from = MB ? kv_end : min(wq0 + 1, kv_end);
     const int qpos = wq0 + c;
     const bool qvalid = qpos < n;
@@ -303,8 +384,9 @@ prefill_attention_kernel(PrefillParams p) {
     // row s / CPR (K rows first, then V rows), physical chunk s % CPR, holding logical chunk
     // (physical ^ swizzle(row)) of key tile * kTile + row
     const char *kbase = p.k + (slot * p.k_sb + h * p.k_sh) * 2;
-    const char *vbase = p.v + (slot * p.v_sb + h * p.v_sh) * 2;
-    const uint32_t kst = (uint32_t)(p.k_st * 2), vst = (uint32_t)(p.v_st * 2);
+    const char *vbase = MB == 0 && p.nv ? p.nv + ((int64_t)t0 * p.nv_st + h * p.nv_sh) * 2
+                                        : p.v + (slot * p.v_sb + h * p.v_sh) * 2;
+    const uint32_t kst = (uint32_t)(p.k_st * 2), vst = (uint32_t)((MB == 0 && p.nv ? p.nv_st : p.v_st) * 2);
     const i32x4_t krs = scalar_rsrc(kbase, kv_end > 0 ? (uint32_t)((kv_end - 1) * kst + D * 2) : 0u);
     const i32x4_t vrs = scalar_rsrc(vbase, kv_end > 0 ? (uint32_t)((kv_end - 1) * vst + D * 2) : 0u);
     // mask rows of the request's queries (rows past its queries read zeros)
@@ -554,16 +636,19 @@ extern "C" int q3t_prefill_rope_write(const q3t_prefill_rope_write_args *a, void
     if (a->total_tokens == 0) return Q3T_OK;
     // q_out == NULL: keys and values only (the attention kernel rotates the queries itself)
     const bool with_q = a->q_out != nullptr;
-    if (!a->cu_seqlens || (with_q && !a->query) || !a->key || !a->value || !a->cos || !a->sin ||
-        !a->arena_keys || !a->arena_values)
+    // value == NULL: keys only (q3t_prefill_attention then copies the values, new_values)
+    const bool with_v = a->value != nullptr;
+    if (!a->cu_seqlens || (with_q && !a->query) || !a->key || !a->cos || !a->sin || !a->arena_keys ||
+        (with_v && !a->arena_values))
         return Q3T_EINVAL;
     const int64_t st[] = {with_q ? a->q_stride_t : 0, with_q ? a->q_stride_h : 0, a->k_stride_t, a->k_stride_h,
-                          a->v_stride_t, a->v_stride_h, a->cs_stride_t, with_q ? a->qo_stride_t : 0,
-                          with_q ? a->qo_stride_h : 0, a->a_stride_b, a->a_stride_h, a->a_stride_t};
+                          with_v ? a->v_stride_t : 0, with_v ? a->v_stride_h : 0, a->cs_stride_t,
+                          with_q ? a->qo_stride_t : 0, with_q ? a->qo_stride_h : 0, a->a_stride_b,
+                          a->a_stride_h, a->a_stride_t};
     for (int64_t s : st)
         if ((s * 2) % 16) return Q3T_EINVAL;
-    const void *ptrs[] = {with_q ? a->query : a->key, a->key, a->value, a->cos, a->sin,
-                          with_q ? a->q_out : a->key, a->arena_keys, a->arena_values};
+    const void *ptrs[] = {with_q ? a->query : a->key, a->key, with_v ? a->value : a->key, a->cos, a->sin,
+                          with_q ? a->q_out : a->key, a->arena_keys, with_v ? a->arena_values : a->key};
     for (const void *q : ptrs)
         if (!aligned(q, 16)) return Q3T_EINVAL;
     PrefillRopeWriteParams p;
@@ -574,7 +659,7 @@ extern "C" int q3t_prefill_rope_write(const q3t_prefill_rope_write_args *a, void
     p.v_st = a->v_stride_t; p.v_sh = a->v_stride_h;
     p.cs = (const char *)a->cos; p.sn = (const char *)a->sin; p.cs_st = a->cs_stride_t;
     p.qo = (char *)a->q_out; p.qo_st = a->qo_stride_t; p.qo_sh = a->qo_stride_h;
-    p.ak = (char *)a->arena_keys; p.av = (char *)a->arena_values;
+    p.ak = (char *)a->arena_keys; p.av = with_v ? (char *)a->arena_values : nullptr;
     p.a_sb = a->a_stride_b; p.a_sh = a->a_stride_h; p.a_st = a->a_stride_t;
     p.slots = a->kv_slots;
     int64_t blocks = (p.T + 3) / 4;  // one token per wave
@@ -587,10 +672,24 @@ extern "C" int q3t_prefill_rope_write(const q3t_prefill_rope_write_args *a, void
 
 template <int D, int GH>
 static void launch_prefill(const PrefillParams &p, hipStream_t s) {
-    const dim3 grid((uint32_t)p.B * p.nqb * (p.Hq / GH));
-    if (!p.mask) hipLaunchKernelGGL((prefill_attention_kernel<D, GH, 0>), grid, dim3(256), 0, s, p);
-    else if (p.mdt == Q3T_F32) hipLaunchKernelGGL((prefill_attention_kernel<D, GH, 4>), grid, dim3(256), 0, s, p);
-    else hipLaunchKernelGGL((prefill_attention_kernel<D, GH, 2>), grid, dim3(256), 0, s, p);
+    const int64_t hgroups = p.Hq / GH;
+    int64_t wgs = (int64_t)p.B * p.nqb * hgroups;
+    if (p.B <= 64) {
+        // items are numbered densely: a request of L rows has ceil(L / 64) blocks, so there are
+        // at most (T + 63 B) / 64 of them; rounded up to whole rounds of one workgroup per CU,
+        // which keeps the placement of every item as in the full grid
+        const int64_t items = (p.T + (int64_t)(kQBlock - 1) * p.B) / kQBlock;
+        const int64_t round = kXcds * kCusPerXcd;
+        const int64_t bound = (items * hgroups + round - 1) / round * round;
+        if (bound < wgs) wgs = bound;
+    }
+    PrefillParams q = p;
+    q.attn_wgs = (int)wgs;
+    if (p.nv) wgs += (p.T + kCopyTokens - 1) / kCopyTokens;
+    const dim3 grid((uint32_t)wgs);
+    if (!p.mask) hipLaunchKernelGGL((prefill_attention_kernel<D, GH, 0>), grid, dim3(256), 0, s, q);
+    else if (p.mdt == Q3T_F32) hipLaunchKernelGGL((prefill_attention_kernel<D, GH, 4>), grid, dim3(256), 0, s, q);
+    else hipLaunchKernelGGL((prefill_attention_kernel<D, GH, 2>), grid, dim3(256), 0, s, q);
 }
 
 extern "C" int q3t_prefill_attention(const q3t_prefill_args *a, void *stream) {
@@ -625,11 +724,23 @@ extern "C" int q3t_prefill_attention(const q3t_prefill_args *a, void *stream) {
             return Q3T_EINVAL;
         if ((a->max_seqlen - 1) * a->mask_stride_q * es + a->capacity * es > INT32_MAX) return Q3T_EUNSUPPORTED;
     }
+    if (a->new_values) {
+        // value rows of the step's tokens: only for the causal rule (a mask scores every key
+        // of the arena view, beyond the step's rows); 32-bit row offsets from a request's
+        // first token
+        if (a->mask) return Q3T_EINVAL;
+        if (!aligned(a->new_values, 16) || a->nv_stride_t < 0 || a->nv_stride_h < 0 || (a->nv_stride_t * 2) % 16 ||
+            (a->nv_stride_h * 2) % 16)
+            return Q3T_EINVAL;
+        const int64_t rows = a->capacity < a->max_seqlen ? a->capacity : a->max_seqlen;
+        if (rows * a->nv_stride_t * 2 + a->head_dim * 2 > INT32_MAX) return Q3T_EUNSUPPORTED;
+    }
     PrefillParams p;
     p.B = (int)a->batch; p.Hq = (int)a->q_heads; p.Hkv = (int)a->kv_heads;
     p.group = (int)G;
     p.nqb = (int)((a->max_seqlen + kQBlock - 1) / kQBlock);
-    if ((int64_t)p.B * p.nqb * p.Hq > INT32_MAX) return Q3T_EUNSUPPORTED;
+    if ((int64_t)p.B * p.nqb * p.Hq + (a->total_tokens + kCopyTokens - 1) / kCopyTokens > INT32_MAX)
+        return Q3T_EUNSUPPORTED;
     p.scale_log2 = a->scale * kLog2eP;
     p.cu = a->cu_seqlens;
     p.q = (const char *)a->query; p.q_st = a->q_stride_t; p.q_sh = a->q_stride_h;
@@ -645,6 +756,8 @@ extern "C" int q3t_prefill_attention(const q3t_prefill_args *a, void *stream) {
     p.mask = (const char *)a->mask;
     p.mdt = (int)a->mask_dtype;
     p.m_sb = a->mask_stride_b; p.m_sq = a->mask_stride_q;
+    p.nv = (const char *)a->new_values; p.nv_st = a->nv_stride_t; p.nv_sh = a->nv_stride_h;
+    p.attn_wgs = 0;  // set at launch
     hipStream_t s = (hipStream_t)stream;
     // the query heads of a KV head pair up in one workgroup and share its staged K/V tiles
     if (G % 2 == 0) {

@@ -194,9 +194,9 @@ class PackedAttention(torch.nn.Module):
 
     def _prefill(self, query, key, value, cos, sin, cache, batch, length):
         """One layer of a padded prefill batch (PrefillGraph): the module's q/k norms, then the
-        prologue kernel rotating the keys into this layer's planes of the packed cache (the
-        values copied beside them), then causal attention over each row's valid keys with the
-        queries rotated in the kernel.  The layer's mask is not needed: the rows are
+        prologue kernel rotating the keys into this layer's planes of the packed cache, then
+        causal attention over each row's valid keys with the queries rotated in the kernel and
+        the values read from the projection (the same launch copies them into the cache).  The layer's mask is not needed: the rows are
         right-padded prompts and the cache carries their lengths."""
         reference = self.reference
         if reference.training:
@@ -209,9 +209,9 @@ class PackedAttention(torch.nn.Module):
         k = reference.k_norm(key).reshape(tokens, -1, width)
         v = value.reshape(tokens, -1, width)
         c, s = cos.reshape(tokens, width), sin.reshape(tokens, width)
-        prefill_rope_write(q, k, v, c, s, cache.cu_seqlens, planes.keys, planes.values, rotate_query=False)
+        prefill_rope_write(q, k, None, c, s, cache.cu_seqlens, planes.keys, planes.values, rotate_query=False)
         out = prefill_attention(q, planes.keys, planes.values, cache.cu_seqlens, length,
-                                scale=reference.scaling, cos=c, sin=s, kv_lens=cache.kv_lens)
+                                scale=reference.scaling, cos=c, sin=s, kv_lens=cache.kv_lens, new_values=v)
         return reference.o_proj(out.view(batch, length, -1))
 
     def forward(self, hidden_states, position_embeddings, attention_mask, past_key_values=None,

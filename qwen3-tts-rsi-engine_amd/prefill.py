@@ -4,17 +4,20 @@ The reference pads a prompt batch to (Bp, Lp) and runs causal self-attention ove
 then copies each request's valid KV prefix into its arena slot
 (PrefillGraph.compute, qwen3_tts_engine/prefill_graph.py:31-50; ContinuousModel.admit_batch,
 continuous.py:425-473 with copy_packed_prefix, packed_kv.py:6-31).  Here the valid rows are
-packed by ``cu_seqlens`` (no padding), the prologue writes rotated keys and values straight
-into the arena slots, and the attention reads them from there:
+packed by ``cu_seqlens`` (no padding), the prologue writes rotated keys straight into the
+arena slots, and the attention reads them from there:
 
 * ``prefill_rope_write`` - RoPE of query and key rows at positions 0 ... len-1 of each
   request (bf16-exact, as ``rotary``) and the paired K/V write into the arena
-  (kernel ``q3t_prefill_rope_write``); with ``rotate_query=False`` the keys and values only;
+  (kernel ``q3t_prefill_rope_write``); with ``rotate_query=False`` the keys and values only,
+  with ``value=None`` the keys only;
 * ``prefill_attention`` - varlen causal GQA on bf16 MFMA tiles (kernel
   ``q3t_prefill_attention``, re-exported from ``attention``); given cos/sin it rotates the
   raw query rows as it loads them;
-* ``prefill_step`` - one layer: the K/V prologue, then attention over the raw queries with
-  their RoPE applied in the attention kernel (no rotated copy of the queries is written).
+* ``prefill_step`` - one layer: the key prologue, then attention over the raw queries with
+  their RoPE applied in the attention kernel (no rotated copy of the queries is written),
+  reading the values from the projection's rows while the same launch copies them into the
+  arena.
 """
 import torch
 
@@ -35,14 +38,16 @@ def prefill_rope_write(query, key, value, cos, sin, cu_seqlens, key_arena, value
     cos/sin (T, D) rows of each token's position; arena planes (slots, Hkv, C, D).
     Writes rotated keys and values at positions 0 ... len_b-1 of slot b (or kv_slots[b])
     and returns the rotated queries (T, Hq, D), or None with ``rotate_query=False`` (the
-    query rows are then not touched)."""
+    query rows are then not touched).  With ``value=None`` only the keys are written (the
+    values are left to ``prefill_attention(new_values=...)``)."""
     if query.ndim != 3 or key.ndim != 3:
         raise ValueError('expected packed (tokens, heads, head_dim) rows')
     tokens, q_heads, head_dim = query.shape
     kv_heads = key.shape[1]
     _check_packed('query', query, tokens, q_heads, head_dim)
     _check_packed('key', key, tokens, kv_heads, head_dim)
-    _check_packed('value', value, tokens, kv_heads, head_dim)
+    if value is not None:
+        _check_packed('value', value, tokens, kv_heads, head_dim)
     if cos.shape != (tokens, head_dim) or sin.shape != cos.shape or cos.dtype != torch.bfloat16 \
             or sin.dtype != torch.bfloat16 or cos.stride(1) != 1 or sin.stride() != cos.stride():
         raise ValueError('cos/sin must be bf16 (tokens, head_dim) rows')
@@ -58,7 +63,8 @@ def prefill_rope_write(query, key, value, cos, sin, cu_seqlens, key_arena, value
         raise ValueError('kv_slots must be an int64 (B,) tensor')
     if kv_slots is None and key_arena.shape[0] < batch:
         raise ValueError('the arena has fewer slots than requests')
-    device = _lib.require_gpu(query, key, value, cos, sin, cu_seqlens, key_arena, value_arena,
+    device = _lib.require_gpu(query, key, cos, sin, cu_seqlens, key_arena, value_arena,
+                              *([value] if value is not None else []),
                               *([kv_slots] if kv_slots is not None else []))
     if not rotate_query:
         if q_out is not None:
@@ -73,11 +79,14 @@ def prefill_rope_write(query, key, value, cos, sin, cu_seqlens, key_arena, value
     a.cu_seqlens = cu_seqlens.data_ptr()
     a.query, (a.q_stride_t, a.q_stride_h) = query.data_ptr(), query.stride()[:2]
     a.key, (a.k_stride_t, a.k_stride_h) = key.data_ptr(), key.stride()[:2]
-    a.value, (a.v_stride_t, a.v_stride_h) = value.data_ptr(), value.stride()[:2]
+    if value is not None:
+        a.value, (a.v_stride_t, a.v_stride_h) = value.data_ptr(), value.stride()[:2]
     a.cos, a.sin, a.cs_stride_t = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
     if q_out is not None:
         a.q_out, (a.qo_stride_t, a.qo_stride_h) = q_out.data_ptr(), q_out.stride()[:2]
-    a.arena_keys, a.arena_values = key_arena.data_ptr(), value_arena.data_ptr()
+    a.arena_keys = key_arena.data_ptr()
+    if value is not None:
+        a.arena_values = value_arena.data_ptr()
     a.a_stride_b, a.a_stride_h, a.a_stride_t = key_arena.stride()[:3]
     if kv_slots is not None:
         a.kv_slots = kv_slots.data_ptr()
@@ -89,8 +98,10 @@ def prefill_rope_write(query, key, value, cos, sin, cu_seqlens, key_arena, value
 def prefill_step(query, key, value, cos, sin, cu_seqlens, max_seqlen, key_arena, value_arena, *,
                  kv_slots=None, scale=None, out=None):
     """One prefill layer over packed prompts: RoPE, arena write, causal GQA.
-    Returns the attention output (T, Hq, D)."""
-    prefill_rope_write(query, key, value, cos, sin, cu_seqlens, key_arena, value_arena,
+    Returns the attention output (T, Hq, D).  Two launches: the rotated keys into the arena,
+    then attention, which rotates the queries as it loads them, reads the values from
+    ``value`` and copies them into the arena."""
+    prefill_rope_write(query, key, None, cos, sin, cu_seqlens, key_arena, value_arena,
                        kv_slots=kv_slots, rotate_query=False)
     return prefill_attention(query, key_arena, value_arena, cu_seqlens, max_seqlen, scale=scale,
-                             kv_slots=kv_slots, out=out, cos=cos, sin=sin)
+                             kv_slots=kv_slots, out=out, cos=cos, sin=sin, new_values=value)
