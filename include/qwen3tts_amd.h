@@ -44,7 +44,7 @@ extern "C" {
    Python bindings here do the same with this string. */
 const char *q3t_status_string(int status);
 
-/* ABI revision of this header; bumps on any incompatible change.  No counterpart in the
+/* ABI revision of this header (8); bumps on any incompatible change.  No counterpart in the
    reference (its operators are Python functions); the bindings refuse another revision. */
 int q3t_abi_version(void);
 

@@ -118,7 +118,7 @@ class KernelError(RuntimeError):
     """A HIP launch failed after host validation passed."""
 
 
-ABI_VERSION = 7  # q3t_abi_version() of the header these structures mirror
+ABI_VERSION = 8  # q3t_abi_version() of the header these structures mirror
 
 
 def library() -> ctypes.CDLL:

@@ -113,7 +113,7 @@ extern "C" const char *q3t_status_string(int status) {
     }
 }
 
-extern "C" int q3t_abi_version(void) { return 7; }
+extern "C" int q3t_abi_version(void) { return 8; }
 
 extern "C" int q3t_kv_write(const void *keys, const void *values, void *target_keys,
                             void *target_values, const int64_t *positions, int64_t batch,

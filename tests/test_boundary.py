@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol(pkg):
 
 def test_status_strings_and_version(pkg):
     lib = pkg.library()
-    assert lib.q3t_abi_version() == 7
+    assert lib.q3t_abi_version() == 8
     assert lib.q3t_status_string(0) == b"success"
     assert lib.q3t_status_string(-1) == b"invalid argument"
     assert lib.q3t_status_string(-3) == b"workspace missing or too small"
