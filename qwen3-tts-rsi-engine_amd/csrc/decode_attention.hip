@@ -1373,14 +1373,19 @@ static int64_t chunk_count(int64_t batch, int64_t kv_heads, int64_t ctx, int64_t
 // The grid a call runs on (Q3T_GRID_CHUNKED, _BALANCED or _BUNDLED; -1: a requested grid the
 // call does not qualify for).  The bundled grid needs bf16 rows of 128, one query token, at
 // most kBundleMaxBatch requests, q_heads / kv_heads <= 4, and a mask with unit key stride.
-// Automatic choice,
-// measured (bf16, 16/8 heads, fused and unfused): bundled for 64..128 requests over arenas of
-// 1024 to 2047 rows (64 requests over 1024 rows: 27.6 us against 30.0 chunked and 37.9
-// balanced; 128 requests: 50.4 against 52.1 and 54.8); balanced from 2048 rows (128 requests
-// over 4096 rows: 165 against 169 bundled and 187 chunked); chunked below 1024 rows and for
-// fewer requests (128 requests over 512 rows: 32.0 against 33.9 bundled; 32 over 1024: 21.6
-// against 21.8), where the bundled grid's ranking and start-up are not repaid.
-constexpr int64_t kBundleMinCtx = 1024;
+// Automatic choice, measured (bf16, 16/8 heads, 28-layer graphs of fused steps, us per layer,
+// contexts uniform over [ctx/16 or 64, ctx]): bundled from 512 rows up when the requests give
+// at least 192 (request, KV head) items (24 requests over 1024 rows: 19.4 against 21.7
+// balanced and 22.2 chunked; 32 over 512: 13.5 against 16.7 chunked; 128 over 512: 28.6
+// against 33.0; 64 over 1024: 26.1 against 30.3; 96 over 2048: 71.7 against 78.2 balanced),
+// and from 4096 rows only with at least 384 items, where fewer whole requests per workgroup
+// leave the longest ones unbalanced (48 requests: 71.3 against 72.5 balanced; 32 requests:
+// 60.9 against 52.9); chunked below 512 rows (64 requests over 256 rows: 12.6 against 12.9
+// bundled; 128 over 128 rows: 13.0 against 16.3), balanced otherwise from 2048 rows.
+constexpr int64_t kBundleMinCtx = 512;
+constexpr int64_t kBundleMinItems = 192;
+constexpr int64_t kBundleLongCtx = 4096;
+constexpr int64_t kBundleMinItemsLong = 384;
 // A mask on the bundled grid: unit key stride, 4-byte aligned, its words addressed by 32-bit
 // byte offsets.
 static bool bundle_mask_ok(const q3t_decode_args *a) {
@@ -1402,8 +1407,9 @@ static int decode_grid(const q3t_decode_args *a) {
     }
     if (a->splits < 0) return Q3T_GRID_CHUNKED;
     if (a->splits > 0) return Q3T_GRID_BALANCED;
-    if (bundle_ok(a) && a->batch * a->kv_heads >= 2 * kBundleGroups && a->ctx >= kBundleMinCtx &&
-        a->ctx < kBalancedMinCtx)
+    const int64_t items = a->batch * a->kv_heads;
+    if (bundle_ok(a) && a->ctx >= kBundleMinCtx &&
+        items >= (a->ctx >= kBundleLongCtx ? kBundleMinItemsLong : kBundleMinItems))
         return Q3T_GRID_BUNDLED;
     return a->ctx >= kBalancedMinCtx ? Q3T_GRID_BALANCED : Q3T_GRID_CHUNKED;
 }
