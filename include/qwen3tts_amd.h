@@ -125,9 +125,9 @@ int q3t_rope_tables(const int64_t *positions, int64_t n, const float *inv_freq, 
  *     shortest, as the step's `plan` (q3t_decode_plan) bundles them or, without one, as the
  *     workgroup ranks them itself.  A mask needs unit key stride and 4-byte alignment (bf16
  *     masks take a branch-free path).  bf16, head_dim 128, query_len 1,
- *     q_heads / kv_heads <= 4, batch <= 128.  The default from ctx >= 512 when
- *     batch * kv_heads >= 192 (>= 384 from ctx >= 4096): the talker's 512- to 2048-row
- *     arenas.
+ *     q_heads / kv_heads <= 4, batch <= 128.  The default when batch * kv_heads is
+ *     192..511 from ctx >= 512, 512 or more from ctx >= 1024 (the talker step), and 384 or
+ *     more from ctx >= 4096.
  *   - balanced (`splits` workgroups per KV head): the concatenated keys of all requests of a
  *     head cut into equal shares, one per workgroup; the default otherwise for ctx >= 2048.
  *   - chunked: each request's keys cut into chunks of 64-key blocks (at most `max_chunks`

@@ -1373,17 +1373,27 @@ static int64_t chunk_count(int64_t batch, int64_t kv_heads, int64_t ctx, int64_t
 // The grid a call runs on (Q3T_GRID_CHUNKED, _BALANCED or _BUNDLED; -1: a requested grid the
 // call does not qualify for).  The bundled grid needs bf16 rows of 128, one query token, at
 // most kBundleMaxBatch requests, q_heads / kv_heads <= 4, and a mask with unit key stride.
-// Automatic choice, measured (bf16, 16/8 heads, 28-layer graphs of fused steps, us per layer,
-// contexts uniform over [ctx/16 or 64, ctx]): bundled from 512 rows up when the requests give
-// at least 192 (request, KV head) items (24 requests over 1024 rows: 19.4 against 21.7
-// balanced and 22.2 chunked; 32 over 512: 13.5 against 16.7 chunked; 128 over 512: 28.6
-// against 33.0; 64 over 1024: 26.1 against 30.3; 96 over 2048: 71.7 against 78.2 balanced),
-// and from 4096 rows only with at least 384 items, where fewer whole requests per workgroup
-// leave the longest ones unbalanced (48 requests: 71.3 against 72.5 balanced; 32 requests:
-// 60.9 against 52.9); chunked below 512 rows (64 requests over 256 rows: 12.6 against 12.9
-// bundled; 128 over 128 rows: 13.0 against 16.3), balanced otherwise from 2048 rows.
+// Automatic choice, measured (bf16, 16/8 heads, 28-layer graphs of fused steps, us per layer).
+// The bundled grid pairs long requests with short ones, so it wins on ragged contexts; with
+// equal contexts two whole requests per workgroup lose to the chunked grid's one per
+// workgroup, two workgroups per CU (64 requests of 512 keys in a 1024-row arena: 27.2 against
+// 26.5; of 64 keys in a 512-row arena: 10.9 against 8.1).  The host sees the capacity, not
+// the lengths, so:
+//  - 24..63 requests (192..511 (request, KV head) items) from 512 rows: bundled, which beat
+//    the chunked grid on every distribution measured (32 requests of 64 keys: 7.9 against
+//    11.0; 32 over 512 rows, uniform lengths: 13.5 against 16.7; 24 over 1024 rows: 19.4
+//    against 21.7 balanced);
+//  - 64..128 requests from 1024 rows (the talker step's ragged contexts: 26.1 against 30.3
+//    chunked; 96 requests over 2048 rows: 71.7 against 78.2 balanced);
+//  - from 4096 rows only with 384 items or more, where one or two whole requests per
+//    workgroup leave the longest unbalanced (32 requests: 60.9 against 52.9 balanced);
+//  - chunked below 512 rows (64 requests over 256 rows: 12.6 against 12.9 bundled) and for 64
+//    or more requests over 512..1023 rows (the reference's valid-length probes, equal
+//    contexts); balanced otherwise from 2048 rows.
 constexpr int64_t kBundleMinCtx = 512;
 constexpr int64_t kBundleMinItems = 192;
+constexpr int64_t kBundleManyItems = 512;      // 64 requests of 8 KV heads
+constexpr int64_t kBundleManyMinCtx = 1024;
 constexpr int64_t kBundleLongCtx = 4096;
 constexpr int64_t kBundleMinItemsLong = 384;
 // A mask on the bundled grid: unit key stride, 4-byte aligned, its words addressed by 32-bit
@@ -1408,9 +1418,10 @@ static int decode_grid(const q3t_decode_args *a) {
     if (a->splits < 0) return Q3T_GRID_CHUNKED;
     if (a->splits > 0) return Q3T_GRID_BALANCED;
     const int64_t items = a->batch * a->kv_heads;
-    if (bundle_ok(a) && a->ctx >= kBundleMinCtx &&
-        items >= (a->ctx >= kBundleLongCtx ? kBundleMinItemsLong : kBundleMinItems))
-        return Q3T_GRID_BUNDLED;
+    const bool bundled = a->ctx >= kBundleLongCtx ? items >= kBundleMinItemsLong
+                         : items >= kBundleManyItems ? a->ctx >= kBundleManyMinCtx
+                                                     : items >= kBundleMinItems && a->ctx >= kBundleMinCtx;
+    if (bundled && bundle_ok(a)) return Q3T_GRID_BUNDLED;
     return a->ctx >= kBalancedMinCtx ? Q3T_GRID_BALANCED : Q3T_GRID_CHUNKED;
 }
 

@@ -120,9 +120,9 @@ def test_decode_workspace_sizes(pkg):
     Chunked grid: ctx 1024 is 16 blocks of 64 keys, chunks capped by max_chunks, by default
     at ceil(512 / (batch * kv_heads)).  Balanced grid: two state slots per workgroup, by
     default 256 / kv_heads workgroups per head.  Bundled grid: no workspace at all.  Automatic
-    choice: bundled for bf16 single-token launches of up to 128 requests over 512 rows or more
-    with at least 192 (request, KV head) items (384 from 4096 rows), balanced otherwise from
-    2048 rows, chunked otherwise."""
+    choice: bundled for bf16 single-token launches of 24..63 requests (192..511 (request, KV
+    head) items) from 512 rows, of 64..128 requests from 1024 rows, and of 48 or more from 4096
+    rows; balanced otherwise from 2048 rows, chunked otherwise."""
     lib = pkg.library()
     counters = 65536 * 4
     state = 2 * 130 * 4
@@ -132,7 +132,8 @@ def test_decode_workspace_sizes(pkg):
     assert _ws(lib, pkg, 63, 1, 1024) == 0                                           # bundled
     assert _ws(lib, pkg, 24, 1, 512) == 0                                            # bundled
     assert _ws(lib, pkg, 23, 1, 1024) == counters + 23 * 8 * 3 * state               # chunked
-    assert _ws(lib, pkg, 64, 1, 511) == counters + 64 * 8 * 1 * state                # chunked
+    assert _ws(lib, pkg, 64, 1, 1023) == counters + 64 * 8 * 1 * state               # chunked
+    assert _ws(lib, pkg, 63, 1, 511) == counters + 63 * 8 * 2 * state                # chunked
     assert _ws(lib, pkg, 64, 1, 1024, dtype=2) == counters + 64 * 8 * 1 * state      # fp32: chunked
     assert _ws(lib, pkg, 64, 1, 1024, masked=True) == counters + 64 * 8 * 1 * state  # mask: chunked
     assert _ws(lib, pkg, 64, 1, 1024, grid=1) == counters + 64 * 8 * 1 * state       # named chunked
@@ -156,9 +157,10 @@ def test_decode_workspace_sizes(pkg):
 
 def test_decode_grid_choice(pkg):
     """The library's grid choice, without a GPU: the talker step (64 requests, 1024-row arena)
-    runs bundled, also with the reference's mask and from the reference's initial 512-row
-    arena; few requests over long arenas balanced, short arenas and small batches chunked;
-    splits still selects balanced (> 0) or chunked (< 0) under the automatic choice."""
+    runs bundled, also with the reference's mask, and so do 24..63 requests from 512 rows;
+    64 or more requests over 512..1023 rows, short arenas and small batches run chunked, few
+    requests over long arenas balanced; splits still selects balanced (> 0) or chunked (< 0)
+    under the automatic choice."""
     decode_grid_for = pkg.decode_grid_for
     assert decode_grid_for(64, 1, 16, 8, 128, 1024) == "bundled"
     assert decode_grid_for(128, 1, 16, 8, 128, 1500) == "bundled"
@@ -169,8 +171,11 @@ def test_decode_grid_choice(pkg):
     assert decode_grid_for(128, 1, 16, 8, 128, 511) == "chunked"
     assert decode_grid_for(32, 1, 16, 8, 128, 1024) == "bundled"
     assert decode_grid_for(24, 1, 16, 8, 128, 512) == "bundled"
+    assert decode_grid_for(63, 1, 16, 8, 128, 512, masked=True) == "bundled"
     assert decode_grid_for(23, 1, 16, 8, 128, 1024) == "chunked"
-    assert decode_grid_for(64, 1, 16, 8, 128, 512, masked=True) == "bundled"
+    assert decode_grid_for(64, 1, 16, 8, 128, 512) == "chunked"
+    assert decode_grid_for(128, 1, 16, 8, 128, 1023) == "chunked"
+    assert decode_grid_for(128, 1, 16, 8, 128, 3000) == "bundled"
     assert decode_grid_for(64, 2, 16, 8, 128, 1024) == "chunked"
     assert decode_grid_for(64, 1, 16, 8, 128, 1024, masked=True) == "bundled"
     assert decode_grid_for(64, 1, 16, 8, 128, 1024, torch.float32) == "chunked"
