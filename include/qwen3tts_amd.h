@@ -285,7 +285,8 @@ typedef struct q3t_prefill_args {
     const int32_t *cu_seqlens;     /* device (batch + 1), non-decreasing */
     const void *query;             /* (tokens, q_heads, head_dim) bf16 */
     int64_t q_stride_t, q_stride_h;
-    const void *keys, *values;     /* arena views */
+    const void *keys;              /* arena views; `values` is written only with new_values */
+    void *values;
     int64_t k_stride_b, k_stride_h, k_stride_t;
     int64_t v_stride_b, v_stride_h, v_stride_t;
     const int64_t *kv_slots;       /* optional device (batch,) */

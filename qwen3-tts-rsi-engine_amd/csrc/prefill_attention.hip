@@ -154,7 +154,8 @@ struct PrefillParams {
     const int32_t *cu;
     const char *q;
     int64_t q_st, q_sh;
-    const char *k, *v;
+    const char *k;
+    char *v;  // written only with nv (the copy workgroups)
     int64_t k_sb, k_sh, k_st, v_sb, v_sh, v_st;
     int64_t cap;
     const int64_t *slots;
@@ -233,7 +234,7 @@ Q3T_DEVICE void copy_value_rows(const PrefillParams &p, int unit) {
             }
 #pragma unroll
             for (int i = 0; i < PER; ++i)
-                if (dst[i] >= 0) store16((char *)p.v + dst[i], buf[i]);
+                if (dst[i] >= 0) store16(p.v + dst[i], buf[i]);
         }
     }
 }
@@ -744,7 +745,7 @@ extern "C" int q3t_prefill_attention(const q3t_prefill_args *a, void *stream) {
     p.scale_log2 = a->scale * kLog2eP;
     p.cu = a->cu_seqlens;
     p.q = (const char *)a->query; p.q_st = a->q_stride_t; p.q_sh = a->q_stride_h;
-    p.k = (const char *)a->keys; p.v = (const char *)a->values;
+    p.k = (const char *)a->keys; p.v = (char *)a->values;
     p.k_sb = a->k_stride_b; p.k_sh = a->k_stride_h; p.k_st = a->k_stride_t;
     p.v_sb = a->v_stride_b; p.v_sh = a->v_stride_h; p.v_st = a->v_stride_t;
     p.slots = a->kv_slots;
