@@ -783,14 +783,17 @@ decode_balanced_kernel(DecodeParams p) {
 
 // ---- bundled grid: whole requests in length-balanced bundles, bf16 MFMA tiles -------------
 // For arena-sized single-token launches over many requests (the talker step).  The grid is one
-// workgroup per CU: Hkv x M workgroups, workgroup (m, h) owning bundle m of KV head h.  Each
-// wave ranks the requests by length in registers (the positions, one load round trip; no LDS
-// and no barrier) and takes the requests of ranks m, 2M-1-m, 2M+m, 4M-1-m (snake order): the
-// longest requests are paired with the shortest, so bundles carry about the same number of
-// keys, and each request is attended by one workgroup (no cross-workgroup merge, no workspace).
+// workgroup per CU: Hkv x M workgroups, workgroup (m, h) owning bundle m of KV head h, which
+// holds the requests of length ranks m, 2M-1-m, 2M+m, 4M-1-m (snake order): the longest
+// requests are paired with the shortest, so bundles carry about the same number of keys, and
+// each request is attended by one workgroup (no cross-workgroup merge, no workspace).  The
+// bundle's four (request, length) entries come from the step's plan (decode_plan.hip) in the
+// same scalar round trip as the kernel arguments, or, without a plan for this batch, from a
+// ranking of the positions that every wave does in its own LDS copy of the keys.
 //   * K/V rows stream through two LDS stages of 64 keys, 16 per wave, loaded by global-to-LDS
 //     buffer loads one stage ahead of the one being scored; the waits are explicit, and the
-//     stream runs across request boundaries.  The ring and the per-wave request rows keep
+//     stream runs across request boundaries.  Masked launches bring each key's 4-byte mask
+//     word with its rows and add the term to its score.  The ring and the request rows keep
 //     one workgroup per CU.
 //   * each wave scores its 16 keys against the request's G query rows with
 //     v_mfma_f32_16x16x32_bf16 (S^T = K . Q^T: A = 16 key rows from LDS, B = the query rows as
@@ -799,14 +802,13 @@ decode_balanced_kernel(DecodeParams p) {
 //     LDS read, B = the bf16 weights straight from the S^T registers).  Rows sit in LDS with
 //     their 16-byte chunks XOR-swizzled (K chunk ch of row r at ch ^ r, V at ch ^ 2r mod 16),
 //     which keeps both reads on distinct banks.
-//   * every wave loads the rows it needs of its requests (query rows and, fused, the cos/sin
-//     rows and new K/V rows) into its own LDS area ahead of the stream, and rotates a request's
-//     query rows (and, in the wave that attends row L-1, the new key) while the request's
-//     first stage is in flight; fused launches place the new key and value in the ring at row
-//     L-1, so the step's key is attended like any other.
+//   * request k's rows (query rows and, fused, the cos/sin rows and new K/V rows) are loaded by
+//     wave k % 4 into one shared area ahead of the stream and rotated there while the first
+//     stages are in flight; fused launches place the new key and value in the ring at row
+//     L-1, so the step's key is attended like any other, and store them into the arena right
+//     after the first stage's wait (a store shares the load counter that the ring waits on).
 //   * at the end of a request the waves' (max, sum, accumulator) states merge in LDS (two
-//     buffers by request parity); outputs and the new arena rows are stored after the stream,
-//     since a store shares the load counter that the ring waits on.
+//     buffers by request parity); the outputs are stored after the stream.
 constexpr int kBundleGroups = 256;    // workgroups of a launch: one per CU
 constexpr int kBundleMaxBatch = 128;  // requests ranked per launch: two per lane
 constexpr int kBundleMaxSeg = 4;      // requests per bundle

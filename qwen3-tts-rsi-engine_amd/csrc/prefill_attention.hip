@@ -36,12 +36,13 @@ Q3T_DEVICE int request_of(const int32_t *cu, int B, int64_t t) {
 // One wave per token; a lane's work item is 8 dims of each half of one of the token's head
 // rows.  Heads [0, Hq) are query heads (rotated into q_out; absent when q_out is null, the
 // attention kernel then rotates the queries itself); the Hkv heads after them rotate the key
-// and copy the value into the arena at the token's position within its request.  The token's
+// and copy the value into the arena at the token's position within its request (without value
+// rows, p.v null, only the keys: the attention launch copies the values).  The token's
 // request, position and slot are the same for the whole wave: 12.5 -> 12.0 us per layer on
-// the 16-prompt workload against one item per thread with per-lane lookups, and 12.0 -> 11.0 us
-// with the request found by one ballot instead of a binary search of dependent loads.  (Two
-// tokens per wave, the next one's rows requested before the current one's are stored, or
-// non-temporal stores: no gain.)
+// the 16-prompt workload (keys and values) against one item per thread with per-lane lookups,
+// and 12.0 -> 11.0 us with the request found by one ballot instead of a binary search of
+// dependent loads; keys only, 6.5 us.  (Two tokens per wave, the next one's rows requested
+// before the current one's are stored, or non-temporal stores: no gain.)
 __global__ void __launch_bounds__(256) prefill_rope_write_kernel(PrefillRopeWriteParams p) {
     const int vecs = p.D / 16;
     const int qh = p.qo ? p.Hq : 0;  // without q_out only the key/value rows are handled
