@@ -11,14 +11,17 @@
 // two tokens per request (the code predictor's first step, continuous.py:37-40) both are
 // rotated, written at pos[b] - 1 and pos[b], and attended causally.
 //
-// Design (one launch per layer, no per-step preparation): two grids over the same per-range
-// core (PairWork):
-//   * balanced (arena-sized launches, the talker step): each KV head's keys of all requests
-//     are cut into equal shares, one per workgroup, so ragged lengths do not leave the
-//     longest requests to a few workgroups at the end of the launch; the shares are derived
-//     on the device from the positions;
-//   * chunked (small caches, the code predictor): one workgroup per (request, chunk of 64-key
-//     blocks, KV head), whose rows are requested together with its position.
+// Design (one launch per layer): three grids.  The bundled grid (the talker step: whole
+// requests per workgroup, longest paired with shortest, bf16 MFMA tiles fed from an LDS ring;
+// its own section below) reads an optional per-step plan (decode_plan.hip).  The other two
+// share a per-range core (PairWork):
+//   * balanced (long arenas): each KV head's keys of all requests are cut into equal shares,
+//     one per workgroup, so ragged lengths do not leave the longest requests to a few
+//     workgroups at the end of the launch; the shares are derived on the device from the
+//     positions;
+//   * chunked (small caches, the code predictor, short arenas): one workgroup per (request,
+//     chunk of 64-key blocks, KV head), whose rows are requested together with its position.
+// For these two:
 //   * lanes: 16 bytes of one key row per lane (LPK lanes per key); a pass of the workgroup
 //     reads 4 KiB of K and 4 KiB of V, all passes of a block are issued before any math;
 //     large arenas are read with the non-temporal cache policy (each row is read once).
