@@ -13,7 +13,7 @@ import torch
 from transformers.cache_utils import Cache
 
 from . import kv_write
-from .attention import PLAN_MAX_BATCH, decode_plan, plan_shape
+from .attention import PLAN_MAX_BATCH, decode_grid_for, decode_plan, plan_shape
 from .packed_kv import copy_packed_prefix, copy_rows
 
 
@@ -141,13 +141,21 @@ class SlotCache(Cache):
         does).  The reference rebuilds its scatter indices from the positions here
         (continuous.py:147-150); the HIP writer reads the positions directly, and this ranks and
         bundles the step's requests for the bundled grid once for all the step's layers
-        (``decode_plan``).  The plan buffer is allocated on the first call (SlotGraph's eager
-        pass, before capture) and refilled by a kernel after."""
+        (``decode_plan``), when the step's launches take that grid (unmasked over the arena, or
+        masked over the context view); otherwise no plan is made.  The plan buffer is
+        allocated on the first call (SlotGraph's eager pass, before capture) and refilled by a
+        kernel after."""
         positions = self.positions
         batch = positions.shape[0]
         q_heads, kv_heads = _attention_heads(self.arena.reference)
         shape = plan_shape(batch, q_heads, kv_heads) if 0 < batch <= PLAN_MAX_BATCH else None
         if not (positions.is_cuda and positions.ndim == 1 and positions.dtype == torch.int64 and shape):
+            self.plan = None
+            return
+        plane = self.arena.keys[0]
+        if not any(decode_grid_for(batch, 1, q_heads, kv_heads, plane.shape[-1], ctx, plane.dtype,
+                                   masked=masked) == 'bundled'
+                   for ctx, masked in ((self.arena.capacity, False), (self.context_length, True))):
             self.plan = None
             return
         if self._plan is None or tuple(self._plan.shape) != shape or self._plan.device != positions.device:

@@ -233,3 +233,19 @@ def test_talker_step_on_the_bundled_grid_reads_the_step_plan(pkg, device):
         assert np.array_equal(bits(out), bits(expected)), f"step {step}"
         assert np.array_equal(bits(arena.packed), bits(twin_arena.packed)), f"step {step}"
     graph.close()
+
+
+@pytest.mark.parametrize("capacity,batch,planned", [(1024, 64, True), (512, 64, False), (512, 32, True),
+                                                     (256, 32, False)])
+def test_prepare_plans_only_for_the_bundled_grid(pkg, device, capacity, batch, planned):
+    """SlotCache.prepare runs the plan kernel only when the step's launches take the bundled
+    grid (64 requests from 1024 rows, 24..63 from 512 rows); otherwise the cache holds no
+    plan and no plan kernel runs."""
+    model = _model(pkg, device, layers=1)
+    arena = pkg.SlotArena(model, batch, capacity, packed_kv=True)
+    positions = torch.randint(0, capacity, (batch,), generator=torch.Generator().manual_seed(3)).to(device)
+    cache = pkg.SlotCache(arena, positions)
+    cache.prepare()
+    assert (pkg.decode_grid_for(batch, 1, 16, 8, 128, capacity) == 'bundled') == planned
+    assert (cache.plan is not None) == planned
+
