@@ -113,12 +113,17 @@ def prefill_detail(pkg, device, reps=20):
         torch.cuda.synchronize()
         times[attention_only] = start.elapsed_time(stop) * 1e3 / (reps * LAYERS)
     flops = 2 * D * HQ * int((lengths * (lengths + 1)).sum())
+    # the step's query, key, value and output rows (T x (Hq + 2 Hkv + Hq) x D bf16)
+    row_bytes = total * (2 * HQ + 2 * HKV) * D * 2
     return {"workload": "16 prompts, lengths randint(32,513) seed 0, sum %d, 28 layers" % total,
+            "lengths": lengths.tolist(),
             "us_per_layer_rope_write_attention": times[False],
             "us_per_layer_attention": times[True],
             "attention_flops_per_layer": flops,
             "attention_TFLOPs": flops / (times[True] * 1e-6) / 1e12,
-            "mfma_frac_of_2500_TFLOPs": flops / (times[True] * 1e-6) / 2.5e15}
+            "mfma_frac_of_2500_TFLOPs": flops / (times[True] * 1e-6) / 2.5e15,
+            "qkvo_bytes_per_layer": row_bytes,
+            "step_GBs": row_bytes / (times[False] * 1e-6) / 1e9}
 
 
 def predictor_detail(pkg, device, reps=20):
@@ -603,6 +608,7 @@ def main():
         "detail": {"kernel": KERNELS[grid_name],
                    "grid": grid_name,
                    "algorithmic_bytes_per_launch": bytes_per_launch,
+                   "contexts": contexts.tolist(),
                    "us_per_layer_launch": launch_us,
                    "us_per_layer_attention_only": attn_us,
                    "attention_only_GBs": attention_bytes(contexts) / (attn_us * 1e-6) / 1e9,
