@@ -11,7 +11,9 @@ The graph (the contract of continuous.py:172-230 on HIP graphs) is checked three
   arithmetic PackedAttention.forward asks for at the same rounding points): the output to
   max-abs 3e-2 / mean-abs 3e-3 (GEMM accumulation order and fp32 against float64 attention
   are the only differences), the arena bit-exact against the write of every layer's own
-  projected rows;
+  projected rows, and every layer's attention output (the input of its o_proj) within the
+  attention bar (max-abs 2e-2, mean-abs 2e-3) of float64 attention over that layer's own
+  projected query rows and the arena;
 * the mask: not built when every attention layer is wrapped.
 """
 import numpy as np
@@ -23,7 +25,7 @@ from oracle import bf16 as obf16
 from oracle import kv as okv
 from oracle import rope as orope
 from tests._talker import Talker
-from tests._util import bits
+from tests._util import assert_attention_close, bits
 from tests.test_decode_gpu import plan_parts
 
 pytestmark = pytest.mark.gpu
@@ -149,10 +151,12 @@ def test_graph_step_matches_the_oracle(pkg, device, shape):
         # bit-identical to the replay) rotated and written by the oracle
         twin_arena.packed.copy_(arena.packed)
         expected_arena = bits(arena.packed).copy()
-        recorded = []
+        recorded, attended = [], []
         hooks = [layer.self_attn.register_forward_hook(
             lambda module, args, kwargs, out: recorded.append((module, kwargs['hidden_states'])),
             with_kwargs=True) for layer in model.layers]
+        hooks += [layer.self_attn.reference.o_proj.register_forward_hook(
+            lambda module, args, out: attended.append(args[0].detach().clone())) for layer in model.layers]
         with torch.inference_mode():
             twin.inputs.copy_(inputs.to(device))
             twin.positions.copy_(positions.to(device))
@@ -162,14 +166,27 @@ def test_graph_step_matches_the_oracle(pkg, device, shape):
             hook.remove()
         cos, sin = model.rotary_emb(inputs.to(device), rotary.to(device))
         cb, sb = bits(cos[0])[:, :, None, :], bits(sin[0])[:, :, None, :]
+        queries = []
         for index, (module, h) in enumerate(recorded):
             proj = torch.nn.functional.linear(h, module.weight, module.bias)
-            _, k, v = proj.split(module.sizes, dim=-1)
-            k = module.reference.k_norm(k.reshape(batch, 1, -1, module.reference.head_dim))
+            q, k, v = proj.split(module.sizes, dim=-1)
+            head_dim = module.reference.head_dim
+            queries.append(orope.rope_bf16(bits(module.reference.q_norm(q.reshape(batch, 1, -1, head_dim))), cb, sb))
+            k = module.reference.k_norm(k.reshape(batch, 1, -1, head_dim))
             k_rot = orope.rope_bf16(bits(k), cb, sb)
             okv.kv_write(expected_arena[index], expected_arena[layers + index], k_rot.transpose(0, 2, 1, 3),
-                         bits(v.reshape(batch, 1, -1, module.reference.head_dim)).transpose(0, 2, 1, 3),
+                         bits(v.reshape(batch, 1, -1, head_dim)).transpose(0, 2, 1, 3),
                          positions.numpy())
+        # each layer's attention on the eager twin (bit-identical to the replay) against float64
+        # attention over its own rotated query rows and the arena it wrote
+        assert len(attended) == layers
+        for index, (module, _) in enumerate(recorded):
+            head_dim = module.reference.head_dim
+            expected_attn = oatt.decode_attention(
+                obf16.from_bits(queries[index]), obf16.from_bits(expected_arena[index][:batch]),
+                obf16.from_bits(expected_arena[layers + index][:batch]), positions.numpy(), module.reference.scaling)
+            got = attended[index].float().cpu().numpy().astype(np.float64).reshape(expected_attn.shape)
+            assert_attention_close(got, expected_attn)
         out = graph.run(inputs.to(device), positions.to(device), rotary.to(device))
         torch.cuda.synchronize()
         assert np.array_equal(bits(arena.packed), expected_arena), f"step {step}"
